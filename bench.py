@@ -1,0 +1,287 @@
+#!/usr/bin/env python
+"""bench.py — MI355X measurement of vkflame's quantized-linear hot path.
+
+One step = one pass of the hot path over one batch: the Q4_K decode GEMV of
+the 14B-class FFN (W 13824x5120 Q4_K, x fp16 [1, 5120], y fp32), reading its
+weights cold from HBM.  Weight copies rotate through more than 1 GiB so the
+256 MB Infinity Cache never holds the step's weights.  The K timed launches
+are captured once in a HIP graph and replayed, bracketed by
+torch.cuda.synchronize() and HIP events on the launch stream.
+
+Prints ONE JSON line (the benchmark contract) with:
+  value      effective weight GB/s of the primary step (BASELINE metric),
+  roofline   the GEMV kernel's algorithmic bytes (weights + x + y) per launch
+             / its measured average duration, against 8 TB/s HBM,
+  cpu_baseline  the numpy port (oracle/oracle.py) on the same workload,
+  suite      every BASELINE configuration (GEMV GB/s and GEMM TOPS with the
+             fraction of the MI355X roofline), measured the same way.
+Diagnostics go to stderr.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q4_K/Q8_0 GEMV weight GB/s + int8/fp16 GEMM TOPS, % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+INT8_PEAK_TOPS = 5000.0
+ROTATE_BYTES = 1 << 30
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _seed(cfg, sub=0):
+    return 1000 + 10 * cfg + sub
+
+
+class Runner:
+    """Captures a list of launches in one HIP graph and times replays."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time_graph(self, launches, reps: int, warmup: int = 2) -> float:
+        """Average ms per launch over `reps` replays of a graph holding
+        `launches` (a list of zero-argument callables)."""
+        torch = self.torch
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for f in launches[:2]:      # eager warm-up (module load, first-touch)
+                f()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for f in launches:
+                f()
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (reps * len(launches))
+
+
+def _rotating_copies(torch, base, nbytes_each):
+    n = max(2, int(ROTATE_BYTES // max(nbytes_each, 1)) + 1)
+    copies = [base]
+    for _ in range(n - 1):
+        copies.append(base.clone())
+    return copies
+
+
+def gemv_case(torch, ops, O, qt, N, K, M, xkind, seed, reps, quant_on_gpu=False):
+    """Returns (ms per launch, weight bytes, algorithmic bytes per launch)."""
+    import numpy as np
+    dev = torch.device("cuda:0")
+    w = torch.from_numpy(O.gen_weight(qt, N, K, seed)).to(dev)
+    wbytes = w.numel()
+    copies = _rotating_copies(torch, w, wbytes)
+    rng = np.random.default_rng(seed + 1)
+    x32 = rng.normal(0, 1, (M, K)).astype(np.float32)
+    if xkind == "f16":
+        x = torch.from_numpy(x32.astype(np.float16)).to(dev)
+        xbytes = M * K * 2
+    elif xkind == "f32":
+        x = torch.from_numpy(x32).to(dev)
+        xbytes = M * K * 4
+    else:
+        xf = torch.from_numpy(x32).to(dev)
+        x = ops.quantize_q8_1(xf)
+        xbytes = M * (K // 32) * 36
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    launches = [(lambda c=c: ops.gemm_q(c, qt, x, N, K, out=y)) for c in copies]
+    ms = Runner(torch).time_graph(launches, reps)
+    t_q = None
+    if quant_on_gpu:
+        t_q = Runner(torch).time_graph([lambda: ops.quantize_q8_1(xf)] * 8, reps)
+    del copies, w
+    torch.cuda.empty_cache()
+    return ms, wbytes, wbytes + xbytes + M * N * 4, t_q
+
+
+def run_suite(torch, ops, O, reps):
+    import numpy as np
+    dev = torch.device("cuda:0")
+    out = []
+
+    def gemv_line(name, qt, N, K, M, xkind, cfg, sub, quant=False):
+        ms, wb, ab, tq = gemv_case(torch, ops, O, qt, N, K, M, xkind, _seed(cfg, sub), reps, quant)
+        gbs = wb / (ms * 1e-3) / 1e9
+        line = {"config": name, "kernel_us": round(ms * 1e3, 2), "weight_GBps": round(gbs, 1),
+                "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                "algorithmic_GBps": round(ab / (ms * 1e-3) / 1e9, 1)}
+        if tq is not None:
+            line["q8_1_quantize_us"] = round(tq * 1e3, 2)
+            line["with_quantize_weight_GBps"] = round(wb / ((ms + tq) * 1e-3) / 1e9, 1)
+        log(json.dumps(line))
+        out.append(line)
+
+    gemv_line("C1 Q8_0 GEMV 4096x4096 M=1 x fp32", O.Q8_0, 4096, 4096, 1, "f32", 1, 0)
+    for qt, nm in ((O.Q4_0, "Q4_0"), (O.Q4_1, "Q4_1")):
+        for M in (1, 4, 16):
+            gemv_line(f"C2 {nm} GEMV 11008x4096 M={M} x fp16", qt, 11008, 4096, M, "f16", 2, qt * 3 + M)
+    for (N, K) in ((13824, 5120), (5120, 13824)):
+        for M in (1, 8):
+            gemv_line(f"C3 Q4_K GEMV {N}x{K} M={M} x fp16", O.Q4_K, N, K, M, "f16", 3, M + (0 if N == 13824 else 5))
+    gemv_line("C5 Q6_K x Q8_1 GEMV 152064x5120 M=1", O.Q6_K, 152064, 5120, 1, "q8_1", 5, 0, quant=True)
+
+    def gemm_line(name, flops, peak, fn_list):
+        ms = Runner(torch).time_graph(fn_list, reps)
+        t = flops / (ms * 1e-3) / 1e12
+        line = {"config": name, "kernel_us": round(ms * 1e3, 2), "TOPS": round(t, 1),
+                "mfma_frac": round(t / peak, 4), "peak_TOPS": peak}
+        log(json.dumps(line))
+        out.append(line)
+
+    # C3 prefill: Q4_K 13824x5120, x fp16 [512, 5120]
+    N, K, M = 13824, 5120, 512
+    w = torch.from_numpy(O.gen_weight(O.Q4_K, N, K, _seed(3))).to(dev)
+    x = torch.from_numpy(np.random.default_rng(_seed(3, 512)).normal(0, 1, (M, K)).astype(np.float16)).to(dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    gemm_line("C3 Q4_K prefill 512x13824x5120 (dequant->LDS fp16 MFMA)", 2.0 * M * N * K, FP16_PEAK_TFLOPS,
+              [lambda: ops.gemm_q(w, O.Q4_K, x, N, K, out=y)] * 4)
+    del w, x, y
+    # C4 int8 linear
+    M, N, K = 512, 5120, 5120
+    inp = O.gen_int8_linear(M, N, K, _seed(4))
+    A, W = torch.from_numpy(inp.A).to(dev), torch.from_numpy(inp.W).to(dev)
+    a_s, w_s = torch.from_numpy(inp.a_scale).to(dev), torch.from_numpy(inp.w_scale).to(dev)
+    bias = torch.from_numpy(inp.bias).to(dev)
+    D = torch.empty((M, N), dtype=torch.float16, device=dev)
+    gemm_line("C4 int8 linear 512x5120x5120 (+scales, bias, fp16 out)", 2.0 * M * N * K, INT8_PEAK_TOPS,
+              [lambda: ops.linear_int8(A, a_s, W, w_s, bias, out=D)] * 4)
+    del A, W, D
+    # C5 prefill: Q6_K x Q8_1, M = 512, full vocab projection
+    N, K, M = 152064, 5120, 512
+    w = torch.from_numpy(O.gen_weight(O.Q6_K, N, K, _seed(5))).to(dev)
+    xf = torch.from_numpy(np.random.default_rng(_seed(5, 1)).normal(0, 1, (M, K)).astype(np.float32)).to(dev)
+    xq = ops.quantize_q8_1(xf)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    gemm_line("C5 Q6_K x Q8_1 prefill 512x152064x5120 (integer-exact MFMA)", 2.0 * M * N * K, INT8_PEAK_TOPS,
+              [lambda: ops.gemm_q(w, O.Q6_K, xq, N, K, out=y)])
+    del w, xf, xq, y
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(O, N, K, wbytes, seed):
+    """The numpy port of the primary step on the host: dequantise the Q4_K
+    weight (oracle.np_dequant) and run x @ W^T through numpy's BLAS."""
+    import numpy as np
+    cores = len(os.sched_getaffinity(0))
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
+    w = O.gen_weight(O.Q4_K, N, K, seed)
+    x = np.random.default_rng(seed + 1).normal(0, 1, (1, K)).astype(np.float16).astype(np.float32)
+    times = []
+    t_end = time.perf_counter() + 20.0
+    while len(times) < 5 and (len(times) < 2 or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        wd = O.np_dequant(O.Q4_K, w).reshape(N, K)
+        _ = x @ wd.T
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    try:
+        import numpy as _np
+        blas = _np.__config__.CONFIG["Build Dependencies"]["blas"]["name"]
+    except Exception:
+        blas = "unknown"
+    return {"value": round(wbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full {N}x{K} Q4_K weight, M=1: numpy dequant (1 thread) + {blas} GEMV, "
+                      f"median of {len(times)} runs, {t * 1e3:.1f} ms each"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-suite", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build's path runs on a single MI355X "
+              f"(got --gpus {args.gpus}); multi-GPU sharding is a design note, not a measured mode.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    from vkflame_amd import ops
+
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(0)
+    log(f"device: {props.name} {props.gcnArchName} CUs={props.multi_processor_count}")
+
+    # ---- primary step: C3 Q4_K decode GEMV 13824x5120, M=1 ----
+    N, K, M = 13824, 5120, 1
+    seed = _seed(3)
+    w = torch.from_numpy(O.gen_weight(O.Q4_K, N, K, seed)).to(dev)
+    wbytes = w.numel()
+    copies = _rotating_copies(torch, w, wbytes)
+    x = torch.from_numpy(np.random.default_rng(seed + 1).normal(0, 1, (M, K)).astype(np.float16)).to(dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    steps = max(len(copies), (args.steps // len(copies)) * len(copies))
+    launches = [(lambda c=copies[i % len(copies)]: ops.gemm_q(c, O.Q4_K, x, N, K, out=y)) for i in range(steps)]
+    r = Runner(torch)
+    ms = r.time_graph(launches, reps=1, warmup=max(1, args.warmup // max(1, steps)))
+    # correctness of the measured configuration (one extra launch, checked on rows)
+    ops.gemm_q(copies[0], O.Q4_K, x, N, K, out=y)
+    torch.cuda.synchronize()
+    rows = np.arange(0, N, 97)
+    ref = O.ref_gemv(x.cpu().numpy().astype(np.float64),
+                     O.np_dequant(O.Q4_K, w.cpu().numpy()[rows]).reshape(len(rows), K))
+    err = O.max_rel_err(y.cpu().numpy()[:, rows], ref)
+    log(f"primary: {ms * 1e3:.2f} us/launch over {steps} launches, {len(copies)} rotating copies, "
+        f"max rel err {err:.2e}")
+    del copies
+    torch.cuda.empty_cache()
+
+    value = wbytes / (ms * 1e-3) / 1e9
+    alg_bytes = wbytes + M * K * 2 + M * N * 4
+    achieved = alg_bytes / (ms * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_q4_k_gemv_13824x5120.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": "vkf_gemv_q4_k_f16", "algorithmic_bytes_per_launch": alg_bytes}
+
+    suite = None if args.no_suite else run_suite(torch, ops, O, reps=20)
+    cpu = None if args.no_cpu else cpu_baseline(O, N, K, wbytes, seed)
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded ggml blocks per BASELINE configs)",
+        "config": {"workload": "C3 Q4_K decode GEMV: W 13824x5120 Q4_K (39.8 MB, cold), x fp16 [1,5120], "
+                               "y fp32 [1,13824]", "global_batch": 1, "seq_len": 1, "parallelism": "single GPU",
+                   "max_rel_err": err},
+        "roofline": roofline, "cpu_baseline": cpu, "suite": suite,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,157 @@
+"""GPU parity: prefill GEMMs on the matrix cores (fp16 MFMA, int8 MFMA,
+dequant-fused quantised GEMM, integer-exact Q6_K x Q8_1) through the C ABI."""
+import numpy as np
+import pytest
+
+import oracle as O
+from _util import TOL_F16, TOL_F32, bits_equal, first_mismatch, rel_err, seed_for, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _f16(rng, *shape):
+    return rng.normal(0, 1, shape).astype(np.float16)
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 32), (200, 72, 40), (17, 300, 1000), (256, 384, 4096)])
+@pytest.mark.parametrize("transA,transB", [(0, 1), (0, 0), (1, 1), (1, 0)])
+def test_linear_fp16_fp32out(dev, M, N, K, transA, transB):
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_FP16_FP32OUT
+    rng = np.random.default_rng(seed_for(4, 40) + M + N + K)
+    A = _f16(rng, M, K)
+    B = _f16(rng, N, K) if transB else _f16(rng, K, N)
+    Am = A.T.copy() if transA else A
+    D = ops.linear(to_dev(Am, dev), to_dev(B, dev), M, N, K, DTYPE_FP16_FP32OUT, transA=transA, transB=transB)
+    torch.cuda.synchronize()
+    Bm = B.T if transB else B
+    ref = A.astype(np.float64) @ Bm.astype(np.float64)
+    assert rel_err(D.cpu().numpy(), ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3])
+def test_linear_fp16_epilogue(dev, act):
+    """fp16 out with alpha, beta*C and every activation."""
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_FP16
+    M, N, K = 96, 160, 256
+    rng = np.random.default_rng(seed_for(4, 50 + act))
+    A, B, C = _f16(rng, M, K), _f16(rng, N, K), _f16(rng, M, N)
+    D = ops.linear(to_dev(A, dev), to_dev(B, dev), M, N, K, DTYPE_FP16, transB=1, act=act,
+                   C=to_dev(C, dev), alpha=0.5, beta=0.25)
+    torch.cuda.synchronize()
+    pre = (0.5 * (A.astype(np.float64) @ B.astype(np.float64).T) + 0.25 * C.astype(np.float64)).astype(np.float32)
+    ref = O.np_act(act, pre)
+    assert rel_err(D.cpu().numpy().astype(np.float32), ref) <= TOL_F16
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (130, 70, 100), (512, 640, 5120)])
+def test_linear_int8_int32_exact(dev, M, N, K):
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_INT8
+    rng = np.random.default_rng(seed_for(4, 60) + M)
+    A = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    D = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8, transB=1)
+    torch.cuda.synchronize()
+    ref = (A.astype(np.float64) @ W.astype(np.float64).T).astype(np.int64)  # exact: |sum| < 2^53
+    assert np.array_equal(D.cpu().numpy().astype(np.int64), ref)
+
+
+def test_config4_linear_int8(dev):
+    """C4: int8 [512,5120] x int8 [5120,5120]^T, per-token and per-channel
+    scales, fp16 bias, fp16 out."""
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_INT8
+    M = 512
+    N = K = 5120
+    inp = O.gen_int8_linear(M, N, K, seed_for(4))
+    A, W = to_dev(inp.A, dev), to_dev(inp.W, dev)
+    acc = ops.linear(A, W, M, N, K, DTYPE_INT8, transB=1)
+    D = ops.linear_int8(A, to_dev(inp.a_scale, dev), W, to_dev(inp.w_scale, dev), to_dev(inp.bias, dev))
+    torch.cuda.synchronize()
+    ref_acc = (inp.A.astype(np.float64) @ inp.W.astype(np.float64).T)
+    assert np.array_equal(acc.cpu().numpy().astype(np.float64), ref_acc)
+    ref = ref_acc * inp.a_scale[:, None].astype(np.float64) * inp.w_scale[None, :].astype(np.float64) \
+        + inp.bias.astype(np.float64)[None, :]
+    assert rel_err(D.cpu().numpy().astype(np.float32), ref) <= TOL_F16
+
+
+@pytest.mark.parametrize("act", [1, 2, 3])
+def test_linear_int8_activation_fp32_out(dev, act):
+    import torch
+    from vkflame_amd import ops
+    M, N, K = 40, 72, 320
+    inp = O.gen_int8_linear(M, N, K, seed_for(4, 70 + act))
+    D = ops.linear_int8(to_dev(inp.A, dev), to_dev(inp.a_scale, dev), to_dev(inp.W, dev),
+                        to_dev(inp.w_scale, dev), to_dev(inp.bias, dev), out_dtype=torch.float32, act=act)
+    torch.cuda.synchronize()
+    _, yref, _ = O.ref_linear_int8(inp, act=act)
+    assert rel_err(D.cpu().numpy(), yref) <= TOL_F32
+
+
+WTYPES = [O.Q4_0, O.Q4_1, O.Q8_0, O.Q5_0, O.Q4_K, O.Q5_K, O.Q6_K]
+
+
+@pytest.mark.parametrize("qt", WTYPES, ids=[O.QNAMES[q] for q in WTYPES])
+def test_gemm_q_fp16_prefill(dev, qt):
+    """M > 16: weight tiles dequantised to fp16 in LDS, fp16 MFMA."""
+    import torch
+    from vkflame_amd import ops
+    M, N, K = 200, 150, 1024
+    w = O.gen_weight(qt, N, K, seed_for(3, 30 + qt))
+    x = _f16(np.random.default_rng(seed_for(3, 40 + qt)), M, K)
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(x, dev), N, K)
+    torch.cuda.synchronize()
+    ref = O.ref_gemv(x.astype(np.float64), O.np_dequant(qt, w).reshape(N, K))
+    assert rel_err(y.cpu().numpy(), ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_K, O.Q8_0], ids=["q4_0", "q4_k", "q8_0"])
+def test_gemm_q_q8_1_activations_prefill(dev, qt):
+    import torch
+    from vkflame_amd import ops
+    M, N, K = 64, 96, 512
+    w = O.gen_weight(qt, N, K, seed_for(3, 50 + qt))
+    x = np.random.default_rng(seed_for(3, 60 + qt)).normal(0, 1, (M, K)).astype(np.float32)
+    xq = O.np_quantize_q8_1(x).reshape(M, -1)
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xq, dev), N, K)
+    torch.cuda.synchronize()
+    x64 = O.np_dequant(O.Q8_1, xq).reshape(M, K).astype(np.float64)
+    assert rel_err(y.cpu().numpy(), O.ref_gemv(x64, O.np_dequant(qt, w).reshape(N, K))) <= TOL_F32
+
+
+def test_config3_q4_k_prefill(dev):
+    """C3 at M=512: 13824x5120 Q4_K, fp16 activations."""
+    import torch
+    from vkflame_amd import ops
+    N, K, M = 13824, 5120, 512
+    w = O.gen_weight(O.Q4_K, N, K, seed_for(3))
+    x = _f16(np.random.default_rng(seed_for(3, 512)), M, K)
+    y = ops.gemm_q(to_dev(w, dev), O.Q4_K, to_dev(x, dev), N, K).cpu().numpy()
+    torch.cuda.synchronize()
+    rows = np.concatenate([[0, N - 1], np.random.default_rng(3).choice(N, 512, replace=False)])
+    wd = O.np_dequant(O.Q4_K, w[rows]).reshape(len(rows), K)
+    assert rel_err(y[:, rows], O.ref_gemv(x.astype(np.float64), wd)) <= TOL_F32
+
+
+def test_config5_q6_k_q8_1_prefill(dev):
+    """C5 at M=512 on a 4096-row slice of the vocab projection (same kernel
+    and per-row work as the full 152064 rows)."""
+    import torch
+    from vkflame_amd import ops
+    N, K, M = 4096, 5120, 512
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(5, 8))
+    x = np.random.default_rng(seed_for(5, 9)).normal(0, 1, (M, K)).astype(np.float32)
+    xq = ops.quantize_q8_1(to_dev(x, dev))
+    y = ops.gemm_q(to_dev(w, dev), O.Q6_K, xq, N, K).cpu().numpy()
+    torch.cuda.synchronize()
+    xq_ref = O.np_quantize_q8_1(x).reshape(M, -1)
+    x64 = O.np_dequant(O.Q8_1, xq_ref).reshape(M, K).astype(np.float64)
+    rows = np.concatenate([[0, N - 1], np.random.default_rng(4).choice(N, 512, replace=False)])
+    wd = O.np_dequant(O.Q6_K, w[rows]).reshape(len(rows), K)
+    assert rel_err(y[:, rows], O.ref_gemv(x64, wd)) <= TOL_F32

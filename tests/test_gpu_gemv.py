@@ -1,0 +1,140 @@
+"""GPU parity: decode GEMV / small GEMM (M <= 16) over ggml weights
+(vkflame_dispatch_gemm_q through the C ABI) against the float64 product of
+the oracle's exact dequantised operands; Q6_K x Q8_1 integer partials
+bit-exact."""
+import numpy as np
+import pytest
+
+import oracle as O
+from _util import TOL_F32, bits_equal, first_mismatch, rel_err, seed_for, to_dev
+
+pytestmark = pytest.mark.gpu
+
+WTYPES = [O.Q4_0, O.Q4_1, O.Q8_0, O.Q5_0, O.Q4_K, O.Q5_K, O.Q6_K]
+
+
+def _x(kind, M, K, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    if kind == "f16":
+        return x.astype(np.float16), x.astype(np.float16).astype(np.float64)
+    if kind == "f32":
+        return x, x.astype(np.float64)
+    q = O.np_quantize_q8_1(x).reshape(M, -1)
+    return q, O.np_dequant(O.Q8_1, q).reshape(M, K).astype(np.float64)
+
+
+@pytest.mark.parametrize("qt", WTYPES, ids=[O.QNAMES[q] for q in WTYPES])
+@pytest.mark.parametrize("kind", ["f16", "f32", "q8_1"])
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_gemv_small(dev, qt, kind, M):
+    import torch
+    from vkflame_amd import ops
+    N, K = 77, 2048 + (256 if O.BLOCK_ELEMS[qt] == 256 else 32)   # ragged N, K not a multiple of 64 chunks
+    w = O.gen_weight(qt, N, K, seed_for(2, qt))
+    xa, x64 = _x(kind, M, K, seed_for(2, 10 + M))
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K)
+    torch.cuda.synchronize()
+    ref = O.ref_gemv(x64, O.np_dequant(qt, w).reshape(N, K))
+    assert rel_err(y.cpu().numpy(), ref) <= TOL_F32
+
+
+def test_gemv_accumulates_into_strided_output(dev):
+    """ldy > N: output rows land at their stride, padding untouched."""
+    import torch
+    from vkflame_amd import ops
+    N, K, M = 64, 512, 4
+    w = O.gen_weight(O.Q4_K, N, K, seed_for(2, 50))
+    xa, x64 = _x("f16", M, K, seed_for(2, 51))
+    ybig = torch.full((M, N + 8), 7.0, device=dev)
+    ops.gemm_q(to_dev(w, dev), O.Q4_K, to_dev(xa, dev), N, K, out=ybig[:, :N])
+    torch.cuda.synchronize()
+    yb = ybig.cpu().numpy()
+    assert np.all(yb[:, N:] == 7.0)
+    assert rel_err(yb[:, :N], O.ref_gemv(x64, O.np_dequant(O.Q4_K, w).reshape(N, K))) <= TOL_F32
+
+
+def _rows_check(y, x64, w, qt, K, rows):
+    wd = O.np_dequant(qt, w[rows]).reshape(len(rows), K)
+    return rel_err(y[:, rows], O.ref_gemv(x64, wd))
+
+
+def test_config1_q8_0_gemv(dev):
+    import torch
+    from vkflame_amd import ops
+    N = K = 4096
+    w = O.gen_weight(O.Q8_0, N, K, seed_for(1))
+    xa, x64 = _x("f32", 1, K, seed_for(1, 1))
+    y = ops.gemm_q(to_dev(w, dev), O.Q8_0, to_dev(xa, dev), N, K)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu().numpy(), O.ref_gemv(x64, O.np_dequant(O.Q8_0, w).reshape(N, K))) <= TOL_F32
+
+
+@pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_1], ids=["q4_0", "q4_1"])
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_config2_q4_gemv(dev, qt, M):
+    import torch
+    from vkflame_amd import ops
+    N, K = 11008, 4096
+    w = O.gen_weight(qt, N, K, seed_for(2, qt))
+    xa, x64 = _x("f16", M, K, seed_for(2, M))
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
+    rows = np.random.default_rng(0).choice(N, 1024, replace=False)
+    rows = np.concatenate([[0, N - 1], rows])
+    assert _rows_check(y, x64, w, qt, K, rows) <= TOL_F32
+
+
+@pytest.mark.parametrize("shape", [(13824, 5120), (5120, 13824)], ids=["13824x5120", "5120x13824"])
+@pytest.mark.parametrize("M", [1, 8])
+def test_config3_q4_k_gemv(dev, shape, M):
+    from vkflame_amd import ops
+    N, K = shape
+    w = O.gen_weight(O.Q4_K, N, K, seed_for(3, 0 if N == 13824 else 1))
+    xa, x64 = _x("f16", M, K, seed_for(3, M))
+    y = ops.gemm_q(to_dev(w, dev), O.Q4_K, to_dev(xa, dev), N, K).cpu().numpy()
+    rows = np.concatenate([[0, N - 1], np.random.default_rng(1).choice(N, 1024, replace=False)])
+    assert _rows_check(y, x64, w, O.Q4_K, K, rows) <= TOL_F32
+
+
+def test_q6_k_q8_1_partials_bit_exact(dev):
+    import torch
+    from vkflame_amd import ops
+    N, K, M = 40, 1024, 5
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(5, 3))
+    xq, _ = _x("q8_1", M, K, seed_for(5, 4))
+    P = ops.q6k_q81_partials(to_dev(w, dev), to_dev(xq, dev), M, N, K)
+    torch.cuda.synchronize()
+    ref = O.c_q6k_q8_1_partials(w, xq, M, N, K)
+    assert bits_equal(P.cpu().numpy(), ref), first_mismatch(P.cpu().numpy(), ref)
+
+
+def test_q6_k_q8_1_partials_extreme_scales(dev):
+    """Scales across the whole int8 range (|sc*(q-32)| up to 4096)."""
+    import torch
+    from vkflame_amd import ops
+    N, K, M = 24, 512, 18   # M > 16 exercises the host's 16-row split
+    rng = np.random.default_rng(seed_for(5, 5))
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(5, 6)).reshape(-1, 210)
+    w[:, 192:208] = rng.integers(-128, 128, (w.shape[0], 16)).astype(np.int8).view(np.uint8)
+    w = w.reshape(N, -1)
+    xq, _ = _x("q8_1", M, K, seed_for(5, 7))
+    P = ops.q6k_q81_partials(to_dev(w, dev), to_dev(xq, dev), M, N, K)
+    torch.cuda.synchronize()
+    assert bits_equal(P.cpu().numpy(), O.c_q6k_q8_1_partials(w, xq, M, N, K))
+
+
+def test_config5_q6_k_q8_1_gemv(dev):
+    """C5 at M=1: fp32 activations quantised on the GPU, vocab projection."""
+    import torch
+    from vkflame_amd import ops
+    N, K = 152064, 5120
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(5))
+    x = np.random.default_rng(seed_for(5, 1)).normal(0, 1, (1, K)).astype(np.float32)
+    xq = ops.quantize_q8_1(to_dev(x, dev))
+    y = ops.gemm_q(to_dev(w, dev), O.Q6_K, xq, N, K).cpu().numpy()
+    torch.cuda.synchronize()
+    xq_ref = O.np_quantize_q8_1(x).reshape(1, -1)
+    assert bits_equal(xq.cpu().numpy(), xq_ref)
+    x64 = O.np_dequant(O.Q8_1, xq_ref).reshape(1, K).astype(np.float64)
+    rows = np.concatenate([[0, N - 1], np.random.default_rng(2).choice(N, 2048, replace=False)])
+    assert _rows_check(y, x64, w, O.Q6_K, K, rows) <= TOL_F32

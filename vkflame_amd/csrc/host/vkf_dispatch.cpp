@@ -1,0 +1,220 @@
+// vkf_dispatch.cpp — the library's C ABI (include/vkflame_amd.h): argument
+// checks, kernel choice and grid math, one hipModuleLaunchKernel per call.
+//
+// Reference counterparts: vkflame_dispatch_dequant (runtime/dispatch.cpp:469-498)
+// and vkflame_dispatch_linear (runtime/dispatch.cpp:253-326).  The reference
+// picks a shader by (dtype, device features) and sizes a 16x16-thread grid;
+// here the choice is by (dtype, quant type, M): M <= 16 is the HBM-bound GEMV
+// regime, larger M the MFMA GEMM regime.
+#include "../../../include/vkflame_amd.h"
+
+#include <cstdint>
+#include <cstdio>
+
+#include "vkf_runtime.h"
+
+namespace {
+
+const int kBlockBytes[8] = {18, 20, 34, 22, 144, 176, 210, 36};
+const int kBlockElems[8] = {32, 32, 32, 32, 256, 256, 256, 32};
+// Byte alignment the decoders assume for a block start (all field loads are
+// 2- or 4-byte loads at fixed offsets inside the block).
+const int kBlockAlign[8] = {2, 4, 2, 2, 4, 4, 2, 4};
+
+inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+inline hipStream_t S(void *s) { return (hipStream_t)s; }
+
+constexpr int kOk = hipSuccess;
+constexpr int kInval = hipErrorInvalidValue;
+constexpr int kNotSup = hipErrorNotSupported;
+
+// Kernel id of GEMV(qt, activation kind 0 fp16 / 1 fp32 / 2 Q8_1).
+VkfKernelId gemv_kernel(int qt, int xk) {
+    static const int order[7] = {VKF_Q4_0, VKF_Q4_1, VKF_Q8_0, VKF_Q5_0, VKF_Q4_K, VKF_Q5_K, VKF_Q6_K};
+    for (int i = 0; i < 7; i++)
+        if (order[i] == qt) return (VkfKernelId)(VKF_K_GEMV_Q4_0_F16 + 3 * i + xk);
+    return VKF_K_COUNT;
+}
+
+// Kernel id of GEMM(qt, activation kind 0 fp16 / 2 Q8_1).
+VkfKernelId gemm_kernel(int qt, int xk) {
+    static const int order[7] = {VKF_Q4_0, VKF_Q4_1, VKF_Q8_0, VKF_Q5_0, VKF_Q4_K, VKF_Q5_K, VKF_Q6_K};
+    for (int i = 0; i < 7; i++)
+        if (order[i] == qt) return (VkfKernelId)(VKF_K_GEMM_Q4_0_F16 + 2 * i + (xk == 2 ? 1 : 0));
+    return VKF_K_COUNT;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *vkflame_version(void) { return "vkflame-amd 0.1 (gfx950)"; }
+
+int vkflame_init(void) {
+    hipFunction_t f;
+    return vkf::get_kernel(VKF_K_QUANT_Q8_1, &f);
+}
+
+int vkflame_block_bytes(int q) { return (q >= 0 && q < 8) ? kBlockBytes[q] : -1; }
+int vkflame_block_elems(int q) { return (q >= 0 && q < 8) ? kBlockElems[q] : -1; }
+
+int vkflame_dispatch_dequant(const void *src, void *dst, uint64_t n_blocks, int qt, int out_dtype, void *stream) {
+    if (qt < 0 || qt > 7) return kInval;
+    if (out_dtype != VKF_DTYPE_FP32 && out_dtype != VKF_DTYPE_FP16) return kInval;
+    if (n_blocks == 0) return kOk;
+    if (!src || !dst || !aligned(src, kBlockAlign[qt]) || !aligned(dst, 16)) return kInval;
+    VkfDequantArgs a{(const uint8_t *)src, dst, n_blocks};
+    uint64_t threads = n_blocks * (uint64_t)(kBlockElems[qt] / 8);
+    if (cdiv(threads, 256) >= 0x7fffffffu) return kInval;
+    VkfKernelId k = (VkfKernelId)(VKF_K_DEQ_Q4_0_F32 + 2 * qt + (out_dtype == VKF_DTYPE_FP16 ? 1 : 0));
+    return vkf::launch(k, dim3(cdiv(threads, 256)), dim3(256), a, S(stream));
+}
+
+int vkflame_quantize_q8_1(const float *x, void *dst, int M, int K, int64_t ldx, void *stream) {
+    if (M < 0 || K < 0 || (K % 32) != 0) return kInval;
+    if (M == 0 || K == 0) return kOk;
+    if (ldx == 0) ldx = K;
+    if (!x || !dst || ldx < K || !aligned(x, 4) || !aligned(dst, 4)) return kInval;
+    VkfQuantizeArgs a{x, (uint8_t *)dst, (uint64_t)ldx, (uint32_t)M, (uint32_t)K};
+    return vkf::launch(VKF_K_QUANT_Q8_1, dim3(cdiv((uint64_t)M * K, 256)), dim3(256), a, S(stream));
+}
+
+int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const void *x, int x_dtype, int64_t ldx,
+                            float *y, int64_t ldy, int M, int N, int K, void *stream) {
+    if (qt < 0 || qt > 6) return kInval;  // Q8_1 is an activation format, not a weight format
+    if (M < 0 || N < 0 || K < 0 || (K % kBlockElems[qt]) != 0) return kInval;
+    if (M == 0 || N == 0) return kOk;
+    const uint64_t packed = (uint64_t)(K / kBlockElems[qt]) * kBlockBytes[qt];
+    if (row_bytes == 0) row_bytes = packed;
+    if (row_bytes < packed || (row_bytes % kBlockAlign[qt]) != 0) return kInval;
+    if (!w || !x || !y || !aligned(w, kBlockAlign[qt])) return kInval;
+    if (ldy == 0) ldy = N;
+    if (ldy < N) return kInval;
+    int xk;
+    if (x_dtype == VKF_DTYPE_FP16) {
+        xk = 0;
+        if (ldx == 0) ldx = K;
+        if (ldx < K) return kInval;
+    } else if (x_dtype == VKF_DTYPE_FP32) {
+        xk = 1;
+        if (ldx == 0) ldx = K;
+        if (ldx < K) return kInval;
+    } else if (x_dtype == VKF_DTYPE_Q8_1) {
+        xk = 2;
+        if (ldx == 0) ldx = (int64_t)(K / 32) * 36;
+        if (ldx < (int64_t)(K / 32) * 36 || (ldx % 4) != 0 || !aligned(x, 4)) return kInval;
+    } else {
+        return kInval;
+    }
+    if (M <= 16) {
+        // GEMV kernels read 16-byte vectors of dense activations.
+        if (xk == 0 && (!aligned(x, 16) || (ldx % 8) != 0)) return kInval;
+        if (xk == 1 && (!aligned(x, 16) || (ldx % 4) != 0)) return kInval;
+        VkfGemvArgs a{(const uint8_t *)w, x, y, row_bytes, (uint64_t)ldx, (uint64_t)ldy,
+                      (uint32_t)M, (uint32_t)N, (uint32_t)K, 0u};
+        return vkf::launch(gemv_kernel(qt, xk), dim3(cdiv(N, 4)), dim3(256), a, S(stream));
+    }
+    if (xk == 1) return kNotSup;  // prefill takes fp16 or Q8_1 activations
+    VkfGemmArgs g{};
+    g.X = x;
+    g.Y = w;
+    g.D = y;
+    g.ldx = (uint64_t)ldx;
+    g.ldy = row_bytes;
+    g.ldd = (uint64_t)ldy;
+    g.R = (uint32_t)M;
+    g.Cn = (uint32_t)N;
+    g.K = (uint32_t)K;
+    g.alpha = 1.0f;
+    g.beta = 0.0f;
+    g.flags = VKF_GF_D_F32;
+    dim3 grid(cdiv(N, 128), cdiv(M, 128));
+    return vkf::launch(gemm_kernel(qt, xk), grid, dim3(256), g, S(stream));
+}
+
+int vkflame_q6_k_q8_1_partials(const void *w, const void *xq, int32_t *P, int M, int N, int K, void *stream) {
+    if (M < 0 || N < 0 || K < 0 || (K % 256) != 0) return kInval;
+    if (M == 0 || N == 0 || K == 0) return kOk;
+    if (!w || !xq || !P || !aligned(w, 2) || !aligned(xq, 4) || !aligned(P, 4)) return kInval;
+    const uint64_t ldx = (uint64_t)(K / 32) * 36;
+    for (int m0 = 0; m0 < M; m0 += 16) {
+        int mb = M - m0 < 16 ? M - m0 : 16;
+        VkfGemvArgs a{(const uint8_t *)w, (const uint8_t *)xq + (uint64_t)m0 * ldx,
+                      (float *)(P + (uint64_t)m0 * N * (K / 32)), (uint64_t)(K / 256) * 210, ldx, 0,
+                      (uint32_t)mb, (uint32_t)N, (uint32_t)K, 0u};
+        int e = vkf::launch(VKF_K_Q6_K_Q8_1_PARTIALS, dim3(cdiv(N, 4)), dim3(256), a, S(stream));
+        if (e != kOk) return e;
+    }
+    return kOk;
+}
+
+int vkflame_dispatch_linear(const void *A, const void *B, const void *C, void *D, int M, int N, int K, int dtype,
+                            int transA, int transB, int activation, const void *alpha, const void *beta,
+                            void *stream) {
+    if (M < 0 || N < 0 || K < 0 || activation < 0 || activation > 3) return kInval;
+    if (M == 0 || N == 0) return kOk;
+    if (!A || !B || !D) return kInval;
+    VkfGemmArgs g{};
+    g.X = A;
+    g.Y = B;
+    g.D = D;
+    g.Cin = C;
+    g.R = (uint32_t)M;
+    g.Cn = (uint32_t)N;
+    g.K = (uint32_t)K;
+    g.ldx = transA ? (uint64_t)M : (uint64_t)K;  // A [M,K] or stored [K,M]
+    g.ldy = transB ? (uint64_t)K : (uint64_t)N;  // B stored [N,K] or [K,N]
+    g.ldd = (uint64_t)N;
+    g.ldc = (uint64_t)N;
+    g.act = (uint32_t)activation;
+    g.flags = (transA ? VKF_GF_X_TRANS : 0u) | (transB ? 0u : VKF_GF_Y_TRANS);
+    dim3 grid(cdiv(N, 128), cdiv(M, 128));
+    if (dtype == VKF_DTYPE_FP16 || dtype == VKF_DTYPE_FP16_FP32OUT) {
+        g.alpha = alpha ? *(const float *)alpha : 1.0f;
+        g.beta = beta ? *(const float *)beta : 0.0f;
+        if (g.beta != 0.0f && !C) return kInval;
+        if (dtype == VKF_DTYPE_FP16_FP32OUT) g.flags |= VKF_GF_D_F32 | VKF_GF_CIN_F32;
+        return vkf::launch(VKF_K_GEMM_F16, grid, dim3(256), g, S(stream));
+    }
+    if (dtype == VKF_DTYPE_INT8) {
+        if (activation != 0) return kInval;
+        g.alpha = alpha ? (float)*(const int32_t *)alpha : 1.0f;
+        g.beta = beta ? (float)*(const int32_t *)beta : 0.0f;
+        if (g.beta != 0.0f && !C) return kInval;
+        g.flags |= VKF_GF_D_I32;
+        return vkf::launch(VKF_K_GEMM_I8, grid, dim3(256), g, S(stream));
+    }
+    return kNotSup;  // FP32 and BF16 GEMM are outside this library's path
+}
+
+int vkflame_dispatch_linear_int8(const int8_t *A, const float *a_scale, const int8_t *W, const float *w_scale,
+                                 const void *bias, int bias_dtype, void *D, int d_dtype, int M, int N, int K,
+                                 int activation, void *stream) {
+    if (M < 0 || N < 0 || K < 0 || activation < 0 || activation > 3) return kInval;
+    if (M == 0 || N == 0) return kOk;
+    if (!A || !W || !D) return kInval;
+    if (d_dtype != VKF_DTYPE_FP16 && d_dtype != VKF_DTYPE_FP32) return kInval;
+    if (bias && bias_dtype != VKF_DTYPE_FP16 && bias_dtype != VKF_DTYPE_FP32) return kInval;
+    VkfGemmArgs g{};
+    g.X = A;
+    g.Y = W;
+    g.D = D;
+    g.rs = a_scale;
+    g.cs = w_scale;
+    g.bias = bias;
+    g.R = (uint32_t)M;
+    g.Cn = (uint32_t)N;
+    g.K = (uint32_t)K;
+    g.ldx = (uint64_t)K;
+    g.ldy = (uint64_t)K;
+    g.ldd = (uint64_t)N;
+    g.act = (uint32_t)activation;
+    g.alpha = 1.0f;
+    g.beta = 0.0f;
+    g.flags = (d_dtype == VKF_DTYPE_FP32 ? VKF_GF_D_F32 : 0u) | (bias_dtype == VKF_DTYPE_FP32 ? VKF_GF_BIAS_F32 : 0u);
+    dim3 grid(cdiv(N, 128), cdiv(M, 128));
+    return vkf::launch(VKF_K_GEMM_I8, grid, dim3(256), g, S(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,153 @@
+// vkf_runtime.cpp — gfx950 code-object loader and launcher.
+//
+// The reference turns SPIR-V blobs into VkPipelines at init
+// (runtime/pipeline.cpp:100-251) and records/submits/waits a command buffer
+// per dispatch (runtime/dispatch.cpp:105-227).  Here the gfx950 code objects
+// built from vkflame_amd/csrc/kernels/*.hip are linked into this library's
+// .rodata (build step: .incbin), loaded with hipModuleLoadData the first time
+// a device needs them, and launched asynchronously on the caller's stream.
+#include "vkf_runtime.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <mutex>
+
+// Generated at build time (vkflame_amd/build.py): one entry per code object.
+struct VkfCodeObject {
+    const char *name;
+    const unsigned char *begin;
+    const unsigned char *end;
+};
+extern "C" const VkfCodeObject vkf_code_objects[];
+extern "C" const int vkf_n_code_objects;
+
+namespace vkf {
+namespace {
+
+const char *const k_names[VKF_K_COUNT] = {
+#define VKF_X(id, sym) sym,
+    VKF_KERNEL_LIST(VKF_X)
+#undef VKF_X
+};
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceTable {
+    std::once_flag once;
+    hipError_t status = hipSuccess;
+    hipFunction_t fn[VKF_K_COUNT] = {};
+    int cus = 0;
+};
+
+DeviceTable g_dev[kMaxDevices];
+
+void load_device(DeviceTable &t, int dev) {
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) { t.status = e; return; }
+    t.cus = prop.multiProcessorCount;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        std::fprintf(stderr, "[vkflame] device %d is %s; this library is built for gfx950 only\n", dev,
+                     prop.gcnArchName);
+        t.status = hipErrorInvalidDeviceFunction;
+        return;
+    }
+    hipModule_t mods[16];
+    int nm = vkf_n_code_objects;
+    for (int i = 0; i < nm; i++) {
+        e = hipModuleLoadData(&mods[i], vkf_code_objects[i].begin);
+        if (e != hipSuccess) {
+            std::fprintf(stderr, "[vkflame] hipModuleLoadData(%s) failed: %s\n", vkf_code_objects[i].name,
+                         hipGetErrorString(e));
+            t.status = e;
+            return;
+        }
+    }
+    for (int k = 0; k < VKF_K_COUNT; k++) {
+        hipFunction_t f = nullptr;
+        for (int i = 0; i < nm && !f; i++) {
+            if (hipModuleGetFunction(&f, mods[i], k_names[k]) != hipSuccess) f = nullptr;
+        }
+        if (!f) {
+            std::fprintf(stderr, "[vkflame] kernel %s missing from the code objects\n", k_names[k]);
+            (void)hipGetLastError();
+            t.status = hipErrorNotFound;
+            return;
+        }
+        t.fn[k] = f;
+    }
+    (void)hipGetLastError();
+}
+
+DeviceTable *table_for_current(hipError_t *err) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        *err = e != hipSuccess ? e : hipErrorInvalidDevice;
+        return nullptr;
+    }
+    DeviceTable &t = g_dev[dev];
+    std::call_once(t.once, load_device, std::ref(t), dev);
+    *err = t.status;
+    return t.status == hipSuccess ? &t : nullptr;
+}
+
+}  // namespace
+
+const char *kernel_name(VkfKernelId id) { return (id >= 0 && id < VKF_K_COUNT) ? k_names[id] : "?"; }
+
+hipError_t get_kernel(VkfKernelId id, hipFunction_t *out) {
+    hipError_t e;
+    DeviceTable *t = table_for_current(&e);
+    if (!t) return e;
+    *out = t->fn[id];
+    return hipSuccess;
+}
+
+int cu_count() {
+    hipError_t e;
+    DeviceTable *t = table_for_current(&e);
+    return t ? t->cus : 256;
+}
+
+hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const void *args, size_t args_size, hipStream_t stream) {
+    (void)args_size;
+    hipFunction_t f;
+    hipError_t e = get_kernel(id, &f);
+    if (e != hipSuccess) return e;
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0) return hipSuccess;  // empty problem
+    if (debug_enabled())
+        debug_log("launch %s grid=(%u,%u,%u) block=(%u,%u,%u) stream=%p", k_names[id], grid.x, grid.y, grid.z,
+                  block.x, block.y, block.z, (void *)stream);
+    void *params[1] = {const_cast<void *>(args)};
+    return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, params, nullptr);
+}
+
+hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream) {
+    if (g.R == 0 || g.Cn == 0) return hipSuccess;
+    dim3 grid((g.Cn + 127) / 128, (g.R + 127) / 128);
+    if (grid.y > 65535) return hipErrorInvalidValue;
+    return launch(id, grid, dim3(256), &g, sizeof(g), stream);
+}
+
+bool debug_enabled() {
+    static const bool on = [] {
+        const char *v = std::getenv("VKFLAME_DEBUG");
+        return v && *v && std::strcmp(v, "0") != 0;
+    }();
+    return on;
+}
+
+void debug_log(const char *fmt, ...) {
+    std::va_list ap;
+    va_start(ap, fmt);
+    std::fputs("[vkflame] ", stderr);
+    std::vfprintf(stderr, fmt, ap);
+    std::fputc('\n', stderr);
+    va_end(ap);
+}
+
+}  // namespace vkf

@@ -1,0 +1,106 @@
+// vkf_runtime.h — internal host runtime: gfx950 code-object loader, kernel
+// table and launcher.  Replaces the reference's Vulkan pipeline table
+// (runtime/pipeline.h:10-44 VKFKernelID, runtime/pipeline.cpp:143-251) and
+// do_dispatch (runtime/dispatch.cpp:105-227): code objects are embedded in the
+// library at build time, loaded once per device with hipModuleLoadData, and
+// every launch is one hipModuleLaunchKernel with a packed kernarg struct on the
+// caller's stream (no descriptor sets, no fence wait).
+#pragma once
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+#include "../include/vkf_kernargs.h"
+
+// Kernel ids.  X-macro: (id, symbol in the code object).
+#define VKF_KERNEL_LIST(X)                                  \
+    X(DEQ_Q4_0_F32, "vkf_dequant_q4_0_f32")                 \
+    X(DEQ_Q4_0_F16, "vkf_dequant_q4_0_f16")                 \
+    X(DEQ_Q4_1_F32, "vkf_dequant_q4_1_f32")                 \
+    X(DEQ_Q4_1_F16, "vkf_dequant_q4_1_f16")                 \
+    X(DEQ_Q8_0_F32, "vkf_dequant_q8_0_f32")                 \
+    X(DEQ_Q8_0_F16, "vkf_dequant_q8_0_f16")                 \
+    X(DEQ_Q5_0_F32, "vkf_dequant_q5_0_f32")                 \
+    X(DEQ_Q5_0_F16, "vkf_dequant_q5_0_f16")                 \
+    X(DEQ_Q4_K_F32, "vkf_dequant_q4_k_f32")                 \
+    X(DEQ_Q4_K_F16, "vkf_dequant_q4_k_f16")                 \
+    X(DEQ_Q5_K_F32, "vkf_dequant_q5_k_f32")                 \
+    X(DEQ_Q5_K_F16, "vkf_dequant_q5_k_f16")                 \
+    X(DEQ_Q6_K_F32, "vkf_dequant_q6_k_f32")                 \
+    X(DEQ_Q6_K_F16, "vkf_dequant_q6_k_f16")                 \
+    X(DEQ_Q8_1_F32, "vkf_dequant_q8_1_f32")                 \
+    X(DEQ_Q8_1_F16, "vkf_dequant_q8_1_f16")                 \
+    X(QUANT_Q8_1, "vkf_quantize_q8_1")                      \
+    /* GEMV: 3 activation kinds per weight type, VKF_Q* order */ \
+    X(GEMV_Q4_0_F16, "vkf_gemv_q4_0_f16")                   \
+    X(GEMV_Q4_0_F32, "vkf_gemv_q4_0_f32")                   \
+    X(GEMV_Q4_0_Q81, "vkf_gemv_q4_0_q8_1")                  \
+    X(GEMV_Q4_1_F16, "vkf_gemv_q4_1_f16")                   \
+    X(GEMV_Q4_1_F32, "vkf_gemv_q4_1_f32")                   \
+    X(GEMV_Q4_1_Q81, "vkf_gemv_q4_1_q8_1")                  \
+    X(GEMV_Q8_0_F16, "vkf_gemv_q8_0_f16")                   \
+    X(GEMV_Q8_0_F32, "vkf_gemv_q8_0_f32")                   \
+    X(GEMV_Q8_0_Q81, "vkf_gemv_q8_0_q8_1")                  \
+    X(GEMV_Q5_0_F16, "vkf_gemv_q5_0_f16")                   \
+    X(GEMV_Q5_0_F32, "vkf_gemv_q5_0_f32")                   \
+    X(GEMV_Q5_0_Q81, "vkf_gemv_q5_0_q8_1")                  \
+    X(GEMV_Q4_K_F16, "vkf_gemv_q4_k_f16")                   \
+    X(GEMV_Q4_K_F32, "vkf_gemv_q4_k_f32")                   \
+    X(GEMV_Q4_K_Q81, "vkf_gemv_q4_k_q8_1")                  \
+    X(GEMV_Q5_K_F16, "vkf_gemv_q5_k_f16")                   \
+    X(GEMV_Q5_K_F32, "vkf_gemv_q5_k_f32")                   \
+    X(GEMV_Q5_K_Q81, "vkf_gemv_q5_k_q8_1")                  \
+    X(GEMV_Q6_K_F16, "vkf_gemv_q6_k_f16")                   \
+    X(GEMV_Q6_K_F32, "vkf_gemv_q6_k_f32")                   \
+    X(GEMV_Q6_K_Q81, "vkf_gemv_q6_k_q8_1_int")              \
+    X(Q6_K_Q8_1_PARTIALS, "vkf_q6_k_q8_1_partials")         \
+    X(GEMM_F16, "vkf_gemm_f16")                             \
+    X(GEMM_I8, "vkf_gemm_i8")                               \
+    /* GEMM: fp16 and Q8_1 activations per weight type */   \
+    X(GEMM_Q4_0_F16, "vkf_gemm_q4_0_f16")                   \
+    X(GEMM_Q4_0_Q81, "vkf_gemm_q4_0_q8_1")                  \
+    X(GEMM_Q4_1_F16, "vkf_gemm_q4_1_f16")                   \
+    X(GEMM_Q4_1_Q81, "vkf_gemm_q4_1_q8_1")                  \
+    X(GEMM_Q8_0_F16, "vkf_gemm_q8_0_f16")                   \
+    X(GEMM_Q8_0_Q81, "vkf_gemm_q8_0_q8_1")                  \
+    X(GEMM_Q5_0_F16, "vkf_gemm_q5_0_f16")                   \
+    X(GEMM_Q5_0_Q81, "vkf_gemm_q5_0_q8_1")                  \
+    X(GEMM_Q4_K_F16, "vkf_gemm_q4_k_f16")                   \
+    X(GEMM_Q4_K_Q81, "vkf_gemm_q4_k_q8_1")                  \
+    X(GEMM_Q5_K_F16, "vkf_gemm_q5_k_f16")                   \
+    X(GEMM_Q5_K_Q81, "vkf_gemm_q5_k_q8_1")                  \
+    X(GEMM_Q6_K_F16, "vkf_gemm_q6_k_f16")                   \
+    X(GEMM_Q6_K_Q81, "vkf_gemm_q6_k_q8_1_int")
+
+enum VkfKernelId {
+#define VKF_X(id, sym) VKF_K_##id,
+    VKF_KERNEL_LIST(VKF_X)
+#undef VKF_X
+    VKF_K_COUNT
+};
+
+namespace vkf {
+
+// Loads the code objects on the current device (once) and returns the kernel.
+hipError_t get_kernel(VkfKernelId id, hipFunction_t *out);
+const char *kernel_name(VkfKernelId id);
+
+// One launch of kernel `id` with a single by-value kernarg struct.
+hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const void *args, size_t args_size,
+                  hipStream_t stream);
+
+template <class T>
+inline hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const T &args, hipStream_t stream) {
+    return launch(id, grid, block, &args, sizeof(T), stream);
+}
+
+// A VkfGemmArgs launch: 128x128 output tile per 256-thread workgroup.
+hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream);
+
+// VKFLAME_DEBUG=1: one stderr line per dispatch (reference: torch_backend/mode.py:13).
+bool debug_enabled();
+void debug_log(const char *fmt, ...);
+
+// Number of compute units of the current device (cached per device).
+int cu_count();
+
+}  // namespace vkf
