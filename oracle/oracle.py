@@ -236,7 +236,8 @@ def np_quantize_q8_1(x: np.ndarray) -> np.ndarray:
     s = (q.sum(axis=1).astype(F32) * d).astype(F32)
     out = np.empty((xb.shape[0], 36), np.uint8)
     out[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
-    out[:, 2:4] = s.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    with np.errstate(over="ignore"):
+        out[:, 2:4] = s.astype(np.float16).view(np.uint8).reshape(-1, 2)
     out[:, 4:36] = q.astype(np.int8).view(np.uint8)
     return out.reshape(-1)
 

@@ -1,0 +1,236 @@
+"""CPU: the C-ABI library loads, exports every symbol the public header
+declares plus the hipBLAS / hipBLASLt entry points, and its host-side logic
+(kernel-name table, BLAS descriptors, argument checks) behaves as specified.
+No call here reaches a GPU: every checked path returns before a launch."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from vkflame_amd import _lib as VL
+from vkflame_amd import lib
+import blas_abi as B
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+HIPBLAS = ["hipblasCreate", "hipblasDestroy", "hipblasSetStream", "hipblasGetStream", "hipblasSetPointerMode",
+           "hipblasGetPointerMode", "hipblasGemmEx", "hipblasGemmBatchedEx", "hipblasGemmStridedBatchedEx",
+           "hipblasHgemm", "hipblasHgemmBatched", "hipblasHgemmStridedBatched"]
+HIPBLASLT = ["hipblasLtCreate", "hipblasLtDestroy", "hipblasLtMatrixLayoutCreate", "hipblasLtMatrixLayoutDestroy",
+             "hipblasLtMatrixLayoutSetAttribute", "hipblasLtMatrixLayoutGetAttribute", "hipblasLtMatmulDescCreate",
+             "hipblasLtMatmulDescDestroy", "hipblasLtMatmulDescSetAttribute", "hipblasLtMatmulDescGetAttribute",
+             "hipblasLtMatmulPreferenceCreate", "hipblasLtMatmulPreferenceDestroy",
+             "hipblasLtMatmulPreferenceSetAttribute", "hipblasLtMatmulAlgoGetHeuristic", "hipblasLtMatmul"]
+
+
+def _declared():
+    txt = open(os.path.join(ROOT, "include", "vkflame_amd.h")).read()
+    return sorted(set(re.findall(r"\b(vkflame_\w+)\s*\(", txt)))
+
+
+def _exported(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    return {l.split()[-1] for l in out.splitlines() if " T " in l}
+
+
+def test_header_symbols_exported():
+    decl = _declared()
+    assert len(decl) >= 10
+    exp = _exported(VL.LIB_PATH)
+    missing = [s for s in decl + HIPBLAS + HIPBLASLT if s not in exp]
+    assert not missing, missing
+    L = lib()
+    for s in decl + HIPBLAS + HIPBLASLT:
+        assert getattr(L, s) is not None
+
+
+def test_library_does_not_interpose_hip_runtime():
+    exp = _exported(VL.LIB_PATH)
+    assert not any(s.startswith("hipLaunch") or s.startswith("hipMalloc") for s in exp)
+
+
+def test_preload_exports_only_hiplaunchkernel():
+    assert _exported(VL.PRELOAD_PATH) == {"hipLaunchKernel"}
+
+
+def test_version_and_block_geometry():
+    L = lib()
+    assert b"gfx950" in L.vkflame_version()
+    assert [L.vkflame_block_bytes(q) for q in range(8)] == [18, 20, 34, 22, 144, 176, 210, 36]
+    assert [L.vkflame_block_elems(q) for q in range(8)] == [32, 32, 32, 32, 256, 256, 256, 32]
+    assert L.vkflame_block_bytes(8) == -1 and L.vkflame_block_elems(-1) == -1
+
+
+# ---------------------------------------------------------------------------
+# kernel-name table (shim/hip_runtime_shim.cpp:896-952, 1096-1188)
+# ---------------------------------------------------------------------------
+
+def P(v):
+    return ctypes.c_void_p(v)
+
+
+def _dq(name, grid=(5, 1, 1), block=(32, 1, 1), nb=7, i64=False):
+    a2 = ctypes.c_int64(nb) if i64 else ctypes.c_int32(nb)
+    return VL.resolve_launch(name, grid, block, [P(0x1000), P(0x2000), a2])
+
+
+@pytest.mark.parametrize("name,qt", [
+    ("_Z21dequantize_block_q4_0PKvPfi", 0), ("dequantize_block_q4K_0", 0), ("dequantize_block_q4_1<float>", 1),
+    ("dequantize_block_q5_0", 3), ("dequantize_block_q5K_0", 3)])
+def test_table_dequant_nb32_rule(name, qt):
+    p = _dq(name, nb=123)
+    assert (p.kind, p.quant_type, p.n_blocks, p.src, p.dst) == (VL.LAUNCH_DEQUANT, qt, 123, 0x1000, 0x2000)
+
+
+def test_table_q8_0_nb_rule():
+    assert _dq("dequantize_block_q8_0", block=(32, 1, 1), nb=77).n_blocks == 77
+    assert _dq("dequantize_block_q8_0", block=(256, 1, 1), nb=32 * 1000, i64=True).n_blocks == 1000
+
+
+@pytest.mark.parametrize("name,qt", [("dequantize_block_q4_K", 4), ("dequantize_block_q4K", 4),
+                                     ("dequantize_block_q5_K", 5), ("dequantize_block_q5K", 5),
+                                     ("dequantize_block_q6_K", 6), ("dequantize_block_q6K", 6)])
+def test_table_k_quants_take_nb_from_grid(name, qt):
+    p = _dq(name, grid=(4242, 1, 1))
+    assert (p.kind, p.quant_type, p.n_blocks) == (VL.LAUNCH_DEQUANT, qt, 4242)
+
+
+def test_table_output_dtype_from_name():
+    assert _dq("_Z21dequantize_block_q4_KI6__halfEvPKvPT_").out_dtype == VL.DTYPE_FP16
+    assert _dq("_Z21dequantize_block_q4_KIDF16_EvPKvPT_").out_dtype == VL.DTYPE_FP16
+    assert _dq("_Z21dequantize_block_q4_KIfEvPKvPT_").out_dtype == VL.DTYPE_FP32
+
+
+def test_table_mul_mat_before_dequant_substrings():
+    args = [P(0x10), P(0x20), P(0x30), ctypes.c_int32(4096), ctypes.c_int32(11008), ctypes.c_int32(4096),
+            ctypes.c_int32(7)]
+    p = VL.resolve_launch("mul_mat_q4_0_q8_1", (1, 1, 1), (64, 1, 1), args)
+    assert (p.kind, p.quant_type, p.K, p.N, p.M) == (VL.LAUNCH_MUL_MAT_Q, 0, 4096, 11008, 7)
+    assert (p.src, p.src1, p.dst) == (0x10, 0x20, 0x30)
+    for nm, qt in [("mul_mat_q4_1", 1), ("mul_mat_vec_q8_0", 2), ("mul_mat_q5_0", 3), ("mul_mat_q4_K", 4),
+                   ("mul_mat_q5_K", 5), ("mul_mat_q6_K", 6)]:
+        assert VL.resolve_launch(nm, (1, 1, 1), (64, 1, 1), args).quant_type == qt
+    pf = VL.resolve_launch("mul_mat_f16", (1, 1, 1), (64, 1, 1), args)
+    assert (pf.kind, pf.M, pf.N, pf.K) == (VL.LAUNCH_MUL_MAT_F16, 7, 11008, 4096)
+
+
+def test_table_falls_through():
+    args = [P(1), P(2), ctypes.c_int32(3), ctypes.c_int32(4), ctypes.c_int32(5), ctypes.c_int32(6),
+            ctypes.c_int32(7)]
+    for nm in ["mul_mat_iq2_xxs_q8_1", "mul_mat_iq4_nl", "get_rows_q4_0", "cpy_f32_q8_0", "softmax_f32",
+               "some_other_kernel", "mul_mat_bf16"]:
+        assert VL.resolve_launch(nm, (1, 1, 1), (64, 1, 1), args).kind == VL.LAUNCH_NONE, nm
+    bad = [P(1), P(2), P(3), ctypes.c_int32(0), ctypes.c_int32(5), ctypes.c_int32(6), ctypes.c_int32(7)]
+    assert VL.resolve_launch("mul_mat_q4_0", (1, 1, 1), (64, 1, 1), bad).kind == VL.LAUNCH_NONE
+
+
+# ---------------------------------------------------------------------------
+# argument checks that return before any launch
+# ---------------------------------------------------------------------------
+
+def test_c_abi_rejects_bad_arguments():
+    L = lib()
+    s = None
+    assert L.vkflame_dispatch_dequant(None, None, 1, 9, 0, s) == 1
+    assert L.vkflame_dispatch_dequant(P(16), P(32), 1, 4, 5, s) == 1         # bad out dtype
+    assert L.vkflame_dispatch_dequant(P(18), P(32), 1, 4, 0, s) == 1         # Q4_K source not 4-aligned
+    assert L.vkflame_dispatch_dequant(P(16), P(40), 1, 0, 0, s) == 1         # dst not 16-aligned
+    assert L.vkflame_dispatch_dequant(None, None, 0, 0, 0, s) == 0           # empty: no-op
+    assert L.vkflame_quantize_q8_1(P(16), P(16), 4, 48, 0, s) == 1            # K % 32
+    assert L.vkflame_quantize_q8_1(P(16), P(16), 4, 64, 32, s) == 1           # ldx < K
+    assert L.vkflame_dispatch_gemm_q(P(16), 4, 0, P(16), 1, 0, P(16), 0, 1, 8, 300, s) == 1   # K % 256
+    assert L.vkflame_dispatch_gemm_q(P(16), 7, 0, P(16), 1, 0, P(16), 0, 1, 8, 256, s) == 1   # Q8_1 weights
+    assert L.vkflame_dispatch_gemm_q(P(16), 4, 0, P(16), 9, 0, P(16), 0, 1, 8, 256, s) == 1   # x dtype
+    assert L.vkflame_dispatch_gemm_q(P(16), 4, 100, P(16), 1, 0, P(16), 0, 1, 8, 256, s) == 1  # row_bytes < packed
+    assert L.vkflame_dispatch_gemm_q(P(16), 4, 0, P(18), 1, 0, P(16), 0, 1, 8, 256, s) == 1   # x misaligned
+    assert L.vkflame_dispatch_gemm_q(P(16), 4, 0, P(16), 1, 0, P(16), 0, 0, 8, 256, s) == 0   # M = 0: no-op
+    assert L.vkflame_dispatch_gemm_q(P(16), 4, 0, P(16), 0, 0, P(16), 0, 32, 8, 256, s) == 801  # fp32 prefill
+    assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 1, 0, 0, 7, None, None, s) == 1
+    assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 0, 0, 0, 0, None, None, s) == 801
+    assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 2, 0, 1, 1, None, None, s) == 1
+    assert L.vkflame_dispatch_linear_int8(P(16), None, P(16), None, None, 1, P(16), 2, 4, 4, 4, 0, s) == 1
+    assert L.vkflame_q6_k_q8_1_partials(P(16), P(16), P(16), 1, 1, 100, s) == 1
+    assert L.vkflame_execute_launch(ctypes.byref(VL.LaunchPlan()), s) == 1
+
+
+# ---------------------------------------------------------------------------
+# hipBLAS / hipBLASLt host objects
+# ---------------------------------------------------------------------------
+
+def test_hipblas_handles_and_errors():
+    L = B.blas()
+    h = ctypes.c_void_p()
+    assert L.hipblasCreate(None) == B.ST_HANDLE_NULL
+    assert L.hipblasCreate(ctypes.byref(h)) == 0
+    assert L.hipblasSetStream(h, P(0x1234)) == 0
+    st = ctypes.c_void_p()
+    assert L.hipblasGetStream(h, ctypes.byref(st)) == 0 and st.value == 0x1234
+    one = ctypes.c_float(1.0)
+    # NULL handle, bad op, bad ld, unsupported type pair: all rejected before a launch
+    args = (B.OP_T, B.OP_N, 8, 8, 8, ctypes.byref(one), P(16), B.R_16F, 8, P(16), B.R_16F, 8, ctypes.byref(one),
+            P(16), B.R_32F, 8, B.COMPUTE_32F, 0)
+    assert L.hipblasGemmEx(None, *args) == B.ST_NOT_INIT
+    assert L.hipblasGemmEx(h, 7, *args[1:]) == 10                                  # INVALID_ENUM
+    bad_ld = list(args); bad_ld[8] = 4
+    assert L.hipblasGemmEx(h, *bad_ld) == B.ST_INVALID_VALUE
+    f32 = list(args); f32[7] = B.R_32F; f32[10] = B.R_32F
+    assert L.hipblasGemmEx(h, *f32) == B.ST_NOT_SUPPORTED
+    empty = list(args); empty[2] = 0
+    assert L.hipblasGemmEx(h, *empty) == B.ST_SUCCESS
+    assert L.hipblasDestroy(h) == 0
+
+
+def test_hipblaslt_descriptors_round_trip():
+    L = B.blas()
+    lay = B.layout(L, B.R_8I, 5120, 512, 5120)
+    buf = ctypes.c_uint64()
+    n = ctypes.c_size_t()
+    assert L.hipblasLtMatrixLayoutGetAttribute(lay, B.LAYOUT_ROWS, ctypes.byref(buf), 8, ctypes.byref(n)) == 0
+    assert buf.value == 5120 and n.value == 8
+    ld = ctypes.c_int64(6000)
+    assert L.hipblasLtMatrixLayoutSetAttribute(lay, B.LAYOUT_LD, ctypes.byref(ld), 8) == 0
+    ld2 = ctypes.c_int64()
+    assert L.hipblasLtMatrixLayoutGetAttribute(lay, B.LAYOUT_LD, ctypes.byref(ld2), 8, None) == 0 and ld2.value == 6000
+    assert L.hipblasLtMatrixLayoutSetAttribute(lay, B.LAYOUT_LD, ctypes.byref(ld), 4) == B.ST_INVALID_VALUE
+    t = ctypes.c_uint32()
+    assert L.hipblasLtMatrixLayoutGetAttribute(lay, B.LAYOUT_TYPE, ctypes.byref(t), 4, None) == 0 and t.value == B.R_8I
+    d = ctypes.c_void_p()
+    assert L.hipblasLtMatmulDescCreate(ctypes.byref(d), B.COMPUTE_32I, B.R_32F) == 0
+    assert B.set_desc(L, d, B.DESC_EPILOGUE, ctypes.c_uint32(B.EPI_GELU_BIAS)) == 0
+    e = ctypes.c_uint32()
+    assert L.hipblasLtMatmulDescGetAttribute(d, B.DESC_EPILOGUE, ctypes.byref(e), 4, None) == 0
+    assert e.value == B.EPI_GELU_BIAS
+    assert B.set_desc(L, d, B.DESC_BIAS_POINTER, P(0xABC0)) == 0
+    bp = ctypes.c_void_p()
+    assert L.hipblasLtMatmulDescGetAttribute(d, B.DESC_BIAS_POINTER, ctypes.byref(bp), 8, None) == 0
+    assert bp.value == 0xABC0
+    h = ctypes.c_void_p()
+    assert L.hipblasLtCreate(ctypes.byref(h)) == 0
+    pref = ctypes.c_void_p()
+    assert L.hipblasLtMatmulPreferenceCreate(ctypes.byref(pref)) == 0
+    ws = ctypes.c_uint64(1 << 20)
+    assert L.hipblasLtMatmulPreferenceSetAttribute(pref, B.PREF_MAX_WORKSPACE, ctypes.byref(ws), 8) == 0
+    res = (B.HeuristicResult * 2)()
+    cnt = ctypes.c_int()
+    assert L.hipblasLtMatmulAlgoGetHeuristic(h, d, lay, lay, lay, lay, pref, 2, res, ctypes.byref(cnt)) == 0
+    assert cnt.value == 1 and res[0].state == 0 and res[0].workspaceSize == 0
+    assert L.hipblasLtMatmulAlgoGetHeuristic(h, d, lay, lay, lay, lay, pref, 0, res, ctypes.byref(cnt)) == 3
+    # shape mismatch and unsupported epilogue are rejected before any launch
+    a = B.layout(L, B.R_8I, 64, 32, 64)
+    b = B.layout(L, B.R_8I, 64, 16, 64)
+    dd = B.layout(L, B.R_16F, 33, 16, 33)
+    one = ctypes.c_float(1.0)
+    assert B.set_desc(L, d, B.DESC_TRANSA, B.OP_T) == 0
+    assert L.hipblasLtMatmul(h, d, ctypes.byref(one), P(16), a, P(16), b, ctypes.byref(one), P(16), dd, P(16), dd,
+                             None, None, 0, None) == B.ST_INVALID_VALUE
+    dd2 = B.layout(L, B.R_16F, 32, 16, 32)
+    assert B.set_desc(L, d, B.DESC_EPILOGUE, ctypes.c_uint32(192)) == 0               # DGELU
+    assert L.hipblasLtMatmul(h, d, ctypes.byref(one), P(16), a, P(16), b, ctypes.byref(one), P(16), dd2, P(16),
+                             dd2, None, None, 0, None) == B.ST_NOT_SUPPORTED
+    for x in (lay, a, b, dd, dd2):
+        assert L.hipblasLtMatrixLayoutDestroy(x) == 0
+    assert L.hipblasLtMatmulDescDestroy(d) == 0
+    assert L.hipblasLtMatmulPreferenceDestroy(pref) == 0
+    assert L.hipblasLtDestroy(h) == 0

@@ -20,6 +20,7 @@
 //    __half/_Float16 instantiation) instead of always fp32;
 //  * unknown and unsupported names (IQ formats) run the original kernel
 //    instead of returning hipSuccess without doing the work;
+//  * a bf16 mul_mat (whose name also contains "f16") is not taken for fp16;
 //  * fp16 mul_mat computes D[M,N] = vy[M,K] . vx[N,K]^T into the fp32 ggml
 //    destination (the reference passed vx as the M-row operand and wrote fp16).
 #include <cstdint>
@@ -83,7 +84,7 @@ int vkflame_resolve_launch(const char *name, unsigned grid_x, unsigned grid_y, u
             if (plan->K < 1 || plan->N < 1 || plan->M < 1) plan->kind = VKF_LAUNCH_NONE;
             return plan->kind;
         }
-        if (n.has("f16") || n.has("fp16")) {  // (1174-1188)
+        if ((n.has("f16") || n.has("fp16")) && !n.has("bf16")) {  // (1174-1188)
             plan->kind = VKF_LAUNCH_MUL_MAT_F16;
             plan->src = arg_ptr(args, 0);
             plan->src1 = arg_ptr(args, 1);
