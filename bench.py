@@ -215,6 +215,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="only run 10 plain device copies of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's path runs on a single MI355X "
@@ -229,6 +231,17 @@ def main():
     from vkflame_amd import ops
 
     dev = torch.device("cuda:0")
+    if args.calib_copy_mib:
+        # A copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch give
+        # the factor between those counters and bytes moved.
+        n = args.calib_copy_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: 10 x {n} bytes")
+        return
     props = torch.cuda.get_device_properties(0)
     log(f"device: {props.name} {props.gcnArchName} CUs={props.multi_processor_count}")
 

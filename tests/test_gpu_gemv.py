@@ -138,3 +138,48 @@ def test_config5_q6_k_q8_1_gemv(dev):
     x64 = O.np_dequant(O.Q8_1, xq_ref).reshape(1, K).astype(np.float64)
     rows = np.concatenate([[0, N - 1], np.random.default_rng(2).choice(N, 2048, replace=False)])
     assert _rows_check(y, x64, w, O.Q6_K, K, rows) <= TOL_F32
+
+
+DOT_TYPES = [O.Q4_0, O.Q4_1, O.Q8_0, O.Q4_K]
+
+
+def _per_row_err(y, x64, w, qt, N, K):
+    ref = O.ref_gemv(x64, O.np_dequant(qt, w).reshape(N, K))
+    return max(rel_err(y[m], ref[m]) for m in range(y.shape[0]))
+
+
+@pytest.mark.parametrize("qt", DOT_TYPES, ids=[O.QNAMES[q] for q in DOT_TYPES])
+@pytest.mark.parametrize("kind", ["f16", "f32"])
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("N", [77, 3001])
+def test_gemv_dot_path(dev, qt, kind, M, N):
+    """The integer dot-product GEMV (K % 64 == 0, M <= 4): every format,
+    activation kind and row-segment width the host picks for small and
+    large N, checked per activation row."""
+    from vkflame_amd import ops
+    K = 1536
+    w = O.gen_weight(qt, N, K, seed_for(2, 20 + qt))
+    xa, x64 = _x(kind, M, K, seed_for(2, 30 + M))
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
+    assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32
+
+
+@pytest.mark.parametrize("qt", DOT_TYPES, ids=[O.QNAMES[q] for q in DOT_TYPES])
+def test_gemv_dot_dynamic_range(dev, qt):
+    """Activations whose 32-element groups span 12 decades, an all-zero row
+    and a row with a single non-zero: each group gets its own exponent."""
+    from vkflame_amd import ops
+    N, K, M = 300, 2048, 4
+    rng = np.random.default_rng(seed_for(2, 40 + qt))
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    x[0] *= np.repeat(10.0 ** rng.uniform(-6, 6, K // 32), 32).astype(np.float32)
+    x[1] = 0.0
+    x[2] = 0.0
+    x[2, 777] = -3.5
+    w = O.gen_weight(qt, N, K, seed_for(2, 50 + qt))
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(x, dev), N, K).cpu().numpy()
+    x64 = x.astype(np.float64)
+    ref = O.ref_gemv(x64, O.np_dequant(qt, w).reshape(N, K))
+    assert np.all(y[1] == 0.0)
+    for m in (0, 2, 3):
+        assert rel_err(y[m], ref[m]) <= TOL_F32, m

@@ -45,6 +45,38 @@ VkfKernelId gemm_kernel(int qt, int xk) {
     return VKF_K_COUNT;
 }
 
+// Dot-product GEMV (kernels/gemv_dot.hip): Q4_0, Q4_1, Q8_0, Q4_K weights,
+// fp16 / fp32 activations, M <= 4.  Chunks are 64 elements; the chunk loads
+// need the row starts aligned as below (36-, 40-, 68- and 144-byte chunks).
+constexpr int kDotWaves = 16;
+constexpr size_t kDotLdsMax = 64 * 1024;
+int dot_format(int qt) {
+    switch (qt) {
+    case VKF_Q4_0: return 0;
+    case VKF_Q4_1: return 1;
+    case VKF_Q8_0: return 2;
+    case VKF_Q4_K: return 3;
+    default: return -1;
+    }
+}
+const uint32_t kDotAlign[4] = {4, 8, 4, 16};
+
+// Lanes per row segment.  A wave tile is (64/S)*rpl rows; a lane walks
+// ceil(C/S) chunks per tile and a wave ceil(tiles/slots) tiles, so the
+// critical path is their product; ties go to the larger S (more tiles).
+uint32_t dot_segment(uint32_t N, uint32_t C, uint32_t rpl, uint32_t slots) {
+    uint32_t best = 64, best_cost = 0xffffffffu;
+    for (uint32_t s = 64; s >= 8; s >>= 1) {
+        const uint32_t tiles = cdiv(N, (64 / s) * rpl);
+        const uint32_t cost = cdiv(tiles, slots) * cdiv(C, s);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = s;
+        }
+    }
+    return best;
+}
+
 }  // namespace
 
 extern "C" {
@@ -113,6 +145,17 @@ int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const voi
         if (xk == 1 && (!aligned(x, 16) || (ldx % 4) != 0)) return kInval;
         VkfGemvArgs a{(const uint8_t *)w, x, y, row_bytes, (uint64_t)ldx, (uint64_t)ldy,
                       (uint32_t)M, (uint32_t)N, (uint32_t)K, 0u};
+        const int fi = dot_format(qt);
+        const size_t lds = (size_t)M * K * 2 + (size_t)M * K / 4;
+        if (fi >= 0 && M <= 4 && xk != 2 && (K % 64) == 0 && lds <= kDotLdsMax && aligned(w, kDotAlign[fi]) &&
+            (row_bytes % kDotAlign[fi]) == 0) {
+            const uint32_t rpl = M == 1 ? 1 : 2, cus = (uint32_t)vkf::cu_count();
+            const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 64), rpl, cus * kDotWaves);
+            const uint32_t tiles = cdiv(N, (64 / seg) * rpl);
+            a.flags |= seg << 8;
+            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_DOT_Q4_0_F16_M1 + 4 * fi + (M == 1 ? 0 : 2) + xk);
+            return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * kDotWaves), a, S(stream), lds);
+        }
         return vkf::launch(gemv_kernel(qt, xk), dim3(cdiv(N, 4)), dim3(256), a, S(stream));
     }
     if (xk == 1) return kNotSup;  // prefill takes fp16 or Q8_1 activations

@@ -113,17 +113,19 @@ int cu_count() {
     return t ? t->cus : 256;
 }
 
-hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const void *args, size_t args_size, hipStream_t stream) {
+hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const void *args, size_t args_size, hipStream_t stream,
+                  size_t shmem) {
     (void)args_size;
     hipFunction_t f;
     hipError_t e = get_kernel(id, &f);
     if (e != hipSuccess) return e;
     if (grid.x == 0 || grid.y == 0 || grid.z == 0) return hipSuccess;  // empty problem
     if (debug_enabled())
-        debug_log("launch %s grid=(%u,%u,%u) block=(%u,%u,%u) stream=%p", k_names[id], grid.x, grid.y, grid.z,
-                  block.x, block.y, block.z, (void *)stream);
+        debug_log("launch %s grid=(%u,%u,%u) block=(%u,%u,%u) lds=%zu stream=%p", k_names[id], grid.x, grid.y,
+                  grid.z, block.x, block.y, block.z, shmem, (void *)stream);
     void *params[1] = {const_cast<void *>(args)};
-    return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, params, nullptr);
+    return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, (unsigned)shmem, stream,
+                                 params, nullptr);
 }
 
 hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream) {

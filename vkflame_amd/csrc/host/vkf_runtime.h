@@ -53,6 +53,23 @@
     X(GEMV_Q6_K_F32, "vkf_gemv_q6_k_f32")                   \
     X(GEMV_Q6_K_Q81, "vkf_gemv_q6_k_q8_1_int")              \
     X(Q6_K_Q8_1_PARTIALS, "vkf_q6_k_q8_1_partials")         \
+    /* dot-product GEMV: per format {f16, f32} x {m1, m4} */ \
+    X(GEMV_DOT_Q4_0_F16_M1, "vkf_gemv_dot_q4_0_f16_m1") \
+    X(GEMV_DOT_Q4_0_F32_M1, "vkf_gemv_dot_q4_0_f32_m1") \
+    X(GEMV_DOT_Q4_0_F16_M4, "vkf_gemv_dot_q4_0_f16_m4") \
+    X(GEMV_DOT_Q4_0_F32_M4, "vkf_gemv_dot_q4_0_f32_m4") \
+    X(GEMV_DOT_Q4_1_F16_M1, "vkf_gemv_dot_q4_1_f16_m1") \
+    X(GEMV_DOT_Q4_1_F32_M1, "vkf_gemv_dot_q4_1_f32_m1") \
+    X(GEMV_DOT_Q4_1_F16_M4, "vkf_gemv_dot_q4_1_f16_m4") \
+    X(GEMV_DOT_Q4_1_F32_M4, "vkf_gemv_dot_q4_1_f32_m4") \
+    X(GEMV_DOT_Q8_0_F16_M1, "vkf_gemv_dot_q8_0_f16_m1") \
+    X(GEMV_DOT_Q8_0_F32_M1, "vkf_gemv_dot_q8_0_f32_m1") \
+    X(GEMV_DOT_Q8_0_F16_M4, "vkf_gemv_dot_q8_0_f16_m4") \
+    X(GEMV_DOT_Q8_0_F32_M4, "vkf_gemv_dot_q8_0_f32_m4") \
+    X(GEMV_DOT_Q4_K_F16_M1, "vkf_gemv_dot_q4_k_f16_m1") \
+    X(GEMV_DOT_Q4_K_F32_M1, "vkf_gemv_dot_q4_k_f32_m1") \
+    X(GEMV_DOT_Q4_K_F16_M4, "vkf_gemv_dot_q4_k_f16_m4") \
+    X(GEMV_DOT_Q4_K_F32_M4, "vkf_gemv_dot_q4_k_f32_m4") \
     X(GEMM_F16, "vkf_gemm_f16")                             \
     X(GEMM_I8, "vkf_gemm_i8")                               \
     /* GEMM: fp16 and Q8_1 activations per weight type */   \
@@ -86,11 +103,12 @@ const char *kernel_name(VkfKernelId id);
 
 // One launch of kernel `id` with a single by-value kernarg struct.
 hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const void *args, size_t args_size,
-                  hipStream_t stream);
+                  hipStream_t stream, size_t shmem = 0);
 
 template <class T>
-inline hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const T &args, hipStream_t stream) {
-    return launch(id, grid, block, &args, sizeof(T), stream);
+inline hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const T &args, hipStream_t stream,
+                         size_t shmem = 0) {
+    return launch(id, grid, block, &args, sizeof(T), stream, shmem);
 }
 
 // A VkfGemmArgs launch: 128x128 output tile per 256-thread workgroup.
