@@ -49,7 +49,11 @@ VkfKernelId gemm_kernel(int qt, int xk) {
 // fp16 / fp32 activations, M <= 4.  Chunks are 64 elements; the chunk loads
 // need the row starts aligned as below (36-, 40-, 68- and 144-byte chunks).
 constexpr int kDotWaves = 16;
-constexpr size_t kDotLdsMax = 64 * 1024;
+// LDS image per workgroup: 8 planes of 4 KiB per reserved activation row
+// plus a 4 KiB table of per-chunk scales and sums (kernels/gemv_dot.hip),
+// for up to 256 chunks of 64 elements.
+constexpr size_t kDotLdsM1 = 8 * 4096 + 4096, kDotLdsM4 = 4 * (8 * 4096 + 4096);
+constexpr int kDotMaxK = 256 * 64;
 int dot_format(int qt) {
     switch (qt) {
     case VKF_Q4_0: return 0;
@@ -146,9 +150,9 @@ int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const voi
         VkfGemvArgs a{(const uint8_t *)w, x, y, row_bytes, (uint64_t)ldx, (uint64_t)ldy,
                       (uint32_t)M, (uint32_t)N, (uint32_t)K, 0u};
         const int fi = dot_format(qt);
-        const size_t lds = (size_t)M * K * 2 + (size_t)M * K / 4;
-        if (fi >= 0 && M <= 4 && xk != 2 && (K % 64) == 0 && lds <= kDotLdsMax && aligned(w, kDotAlign[fi]) &&
-            (row_bytes % kDotAlign[fi]) == 0) {
+        const size_t lds = M == 1 ? kDotLdsM1 : kDotLdsM4;
+        if (fi >= 0 && M <= 4 && xk != 2 && (K % 64) == 0 && K <= kDotMaxK && lds <= vkf::max_lds() &&
+            aligned(w, kDotAlign[fi]) && (row_bytes % kDotAlign[fi]) == 0) {
             const uint32_t rpl = M == 1 ? 1 : 2, cus = (uint32_t)vkf::cu_count();
             const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 64), rpl, cus * kDotWaves);
             const uint32_t tiles = cdiv(N, (64 / seg) * rpl);

@@ -40,6 +40,7 @@ struct DeviceTable {
     hipError_t status = hipSuccess;
     hipFunction_t fn[VKF_K_COUNT] = {};
     int cus = 0;
+    size_t max_lds = 65536;  // dynamic + static LDS one workgroup may use
 };
 
 DeviceTable g_dev[kMaxDevices];
@@ -49,6 +50,7 @@ void load_device(DeviceTable &t, int dev) {
     hipError_t e = hipGetDeviceProperties(&prop, dev);
     if (e != hipSuccess) { t.status = e; return; }
     t.cus = prop.multiProcessorCount;
+    t.max_lds = prop.sharedMemPerBlock;
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         std::fprintf(stderr, "[vkflame] device %d is %s; this library is built for gfx950 only\n", dev,
                      prop.gcnArchName);
@@ -111,6 +113,12 @@ int cu_count() {
     hipError_t e;
     DeviceTable *t = table_for_current(&e);
     return t ? t->cus : 256;
+}
+
+size_t max_lds() {
+    hipError_t e;
+    DeviceTable *t = table_for_current(&e);
+    return t ? t->max_lds : 65536;
 }
 
 hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const void *args, size_t args_size, hipStream_t stream,

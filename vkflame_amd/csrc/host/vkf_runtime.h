@@ -120,5 +120,7 @@ void debug_log(const char *fmt, ...);
 
 // Number of compute units of the current device (cached per device).
 int cu_count();
+// LDS bytes one workgroup may use on the current device.
+size_t max_lds();
 
 }  // namespace vkf

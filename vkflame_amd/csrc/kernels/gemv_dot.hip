@@ -24,16 +24,16 @@
 // it bounds the output error by ~1e-4 of max|y| (1e-3 tolerance).
 //
 // Work split.  One 1024-thread workgroup per CU stages all M activation rows
-// in LDS once, then its 16 waves walk row tiles (tile t -> wave t % (16*G)
-// of workgroup ...).  Inside a wave, segments of S lanes (S = 8..64, host
-// choice) own RPL rows each; lane p of a segment takes the 64-element chunks
-// c = p, p + S, ... of its rows (two groups 2c, 2c+1 per chunk: a Q4_K
-// sub-block pair, or two Q4_0/Q4_1/Q8_0 blocks), reads each chunk's bytes
-// with 128-bit loads, and reuses the chunk's activations for its RPL rows.
-// Partial sums are reduced across the segment with lane shuffles.
+// in LDS once, then its 16 waves walk row tiles.  Inside a wave, segments of
+// S lanes (S = 8..64, host choice) own RPL rows each; lane p of a segment
+// takes the 64-element chunks c = p, p + S, ... of its rows (groups 2c and
+// 2c+1: a Q4_K sub-block pair, or two Q4_0/Q4_1/Q8_0 blocks), reads each
+// chunk's bytes with 128-bit loads and reuses the chunk's activations for
+// its RPL rows.  Partial sums are reduced across the segment with shuffles.
 #include "vkf_device.h"
 
 #define DOT_WAVES 16
+#define DOT_PLANE 4096  // bytes per LDS plane: chunks c < 256, K <= 16384
 
 typedef unsigned int vkf_u4 __attribute__((ext_vector_type(4)));
 typedef unsigned int vkf_u2 __attribute__((ext_vector_type(2)));
@@ -43,82 +43,98 @@ typedef unsigned int vkf_u4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef unsigned int vkf_u2a4 __attribute__((ext_vector_type(2), aligned(4)));
 
 // ---------------------------------------------------------------------------
-// LDS image of the activations.  G = K/32 groups per row, C = G/2 chunks.
-//   xq: for row m, parity b (group 2c+b) and piece q, a plane of C 16-byte
-//       entries; entry c holds piece q of group 2c+b:
-//       q = 0: h[0..15], 1: h[16..31], 2: l[0..15], 3: l[16..31].
-//       (Lanes of a segment read consecutive entries: no bank conflicts.)
-//   xs: one float4 per (m, c): {2^E, fs} of group 2c, then of group 2c+1.
+// LDS image of the activations (MM rows reserved, M staged), one exponent E
+// per 64-element chunk c (groups 2c, 2c+1):
+//   xq: plane (m*8 + b*4 + q) of DOT_PLANE bytes, entry c (16 bytes) holds
+//       piece q of group 2c+b: q = 0: h[0..15], 1: h[16..31], 2: l[0..15],
+//       3: l[16..31].  Lanes of a segment read consecutive entries (no bank
+//       conflicts) and the 8 pieces of a chunk sit at fixed offsets from one
+//       address (immediate ds_read offsets).
+//   xs: after the MM*8 planes, int4 per (m, c): {bits of 2^E, S0, S1, 0},
+//       S_b = sum of v over group 2c+b (|S_b| <= 2^18).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t xq_entry(uint32_t m, uint32_t b, uint32_t q, uint32_t C, uint32_t c) {
-    return ((m * 2 + b) * 4 + q) * C + c;
+template <int MM>
+__device__ __forceinline__ uint32_t xs_offset(uint32_t m, uint32_t c) {
+    return MM * 8 * DOT_PLANE + (m * 256 + c) * 16;
 }
+template <int MM>
+constexpr uint32_t dot_lds_bytes() { return MM * 8 * DOT_PLANE + MM * 256 * 16; }
+
+// Staging.  Item i = 8 consecutive elements of one row (8 items per chunk,
+// K/8 per row, row m = i / (K/8) for M <= 4).  The 8 items of a chunk sit
+// in 8 adjacent lanes (lane groups aligned to 8) and meet through DPP
+// moves: quad_perm within 4 lanes (one group), row_half_mirror between the
+// two quads of the 8.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+#define DPP_XOR1 0xb1        // quad_perm [1,0,3,2]
+#define DPP_XOR2 0x4e        // quad_perm [2,3,0,1]
+#define DPP_HALF_MIRROR 0x141
 
 template <int XK>
-__device__ __forceinline__ void dot_stage_x(const VkfGemvArgs &a, vkf_u4 *xq, vkf_f4 *xs, uint32_t G, uint32_t M) {
-    const uint32_t C = G / 2;
-    const uint32_t items = M * G * 4;  // item = 8 consecutive elements; 4 per group
-    for (uint32_t i0 = 0; i0 < items; i0 += blockDim.x) {
-        const uint32_t i = i0 + threadIdx.x;
-        const bool live = i < items;
-        const uint32_t m = live ? i / (G * 4) : 0;
-        const uint32_t r = live ? i - m * G * 4 : 0;
-        const uint32_t g = r >> 2, qq = r & 3;  // group, eighth of the group
-        float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (live) {
-            const uint64_t off = (uint64_t)m * a.ldx + 32ull * g + 8 * qq;
-            if (XK == 1) {
-                const vkf_f4 *p = (const vkf_f4 *)((const float *)a.x + off);
-                const vkf_f4 p0 = p[0], p1 = p[1];
-                v[0] = p0[0]; v[1] = p0[1]; v[2] = p0[2]; v[3] = p0[3];
-                v[4] = p1[0]; v[5] = p1[1]; v[6] = p1[2]; v[7] = p1[3];
-            } else {
-                const vkf_h8 h = *(const vkf_h8 *)((const _Float16 *)a.x + off);
+__device__ __forceinline__ void dot_load_x(const VkfGemvArgs &a, uint32_t i, uint32_t items, uint32_t K8, float v[8]) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) v[j] = (float)h[j];
-            }
-        }
-        // The 4 items of a group sit in 4 adjacent lanes (blockDim % 4 == 0).
-        float amax = 0.0f;
+    for (int j = 0; j < 8; j++) v[j] = 0.0f;
+    if (i >= items) return;
+    const uint32_t m = (i >= K8) + (i >= 2 * K8) + (i >= 3 * K8), r = i - m * K8;
+    const uint64_t off = (uint64_t)m * a.ldx + 8ull * r;
+    if (XK == 1) {
+        const vkf_f4 *p = (const vkf_f4 *)((const float *)a.x + off);
+        const vkf_f4 p0 = p[0], p1 = p[1];
+        v[0] = p0[0]; v[1] = p0[1]; v[2] = p0[2]; v[3] = p0[3];
+        v[4] = p1[0]; v[5] = p1[1]; v[6] = p1[2]; v[7] = p1[3];
+    } else {
+        const vkf_h8 h = *(const vkf_h8 *)((const _Float16 *)a.x + off);
 #pragma unroll
-        for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[j]));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        int e2;
-        (void)frexpf(amax, &e2);  // amax < 2^e2 (amax == 0: e2 = 0)
-        const int E = e2 - 13;    // |x| * 2^-E < 2^13
-        uint32_t hw[2] = {0, 0}, lw[2] = {0, 0};
-        int sum = 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int vi = (int)rintf(ldexpf(v[j], -E));
-            sum += vi;
-            hw[j >> 2] |= ((uint32_t)(vi >> 7) & 0xffu) << (8 * (j & 3));
-            lw[j >> 2] |= ((uint32_t)vi & 127u) << (8 * (j & 3));
-        }
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        if (live) {
-            const uint32_t c = g >> 1, b = g & 1, q = qq >> 1, half = qq & 1;
-            vkf_u2 *ph = (vkf_u2 *)(xq + xq_entry(m, b, q, C, c)) + half;
-            vkf_u2 *pl = (vkf_u2 *)(xq + xq_entry(m, b, 2 + q, C, c)) + half;
-            *ph = vkf_u2{hw[0], hw[1]};
-            *pl = vkf_u2{lw[0], lw[1]};
-            if (qq == 0) {
-                const float fe = ldexpf(1.0f, E);
-                float *s = (float *)(xs + (uint64_t)m * C + c) + 2 * b;
-                s[0] = fe;
-                s[1] = fe * (float)sum;  // |sum| <= 2^18: exact
-            }
-        }
+        for (int j = 0; j < 8; j++) v[j] = (float)h[j];
     }
 }
 
-// sum over one 32-element group: w[i] holds codes of elements 4i..4i+3.
-__device__ __forceinline__ int group_dot(const uint32_t w[8], const vkf_u4 *xq, uint32_t m, uint32_t b,
-                                         uint32_t C, uint32_t c) {
-    const vkf_u4 h0 = xq[xq_entry(m, b, 0, C, c)], h1 = xq[xq_entry(m, b, 1, C, c)];
-    const vkf_u4 l0 = xq[xq_entry(m, b, 2, C, c)], l1 = xq[xq_entry(m, b, 3, C, c)];
+// Quantise item i and store it; every lane of the wave takes part.
+template <int MM>
+__device__ __forceinline__ void dot_store_x(unsigned char *lds, uint32_t i, uint32_t items, uint32_t K8,
+                                            const float v[8]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, dpp_f<DPP_XOR1>(amax));
+    amax = fmaxf(amax, dpp_f<DPP_XOR2>(amax));
+    amax = fmaxf(amax, dpp_f<DPP_HALF_MIRROR>(amax));
+    // amax < 2^e2 with e2 = biased exponent - 126 (amax == 0 or subnormal:
+    // e2 = -126, still a bound), E = e2 - 13 so that |x| * 2^-E < 2^13.
+    const int E = (int)((__float_as_uint(amax) >> 23) & 0xffu) - 139;
+    uint32_t hw[2] = {0, 0}, lw[2] = {0, 0};
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int vi = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v[j], -E));
+        sum += vi;
+        hw[j >> 2] |= ((uint32_t)(vi >> 7) & 0xffu) << (8 * (j & 3));
+        lw[j >> 2] |= ((uint32_t)vi & 127u) << (8 * (j & 3));
+    }
+    sum += dpp_i<DPP_XOR1>(sum);  // group sums: the quad of items 4b .. 4b+3
+    sum += dpp_i<DPP_XOR2>(sum);
+    const int s1 = dpp_i<DPP_HALF_MIRROR>(sum);
+    if (i < items) {
+        const uint32_t m = (i >= K8) + (i >= 2 * K8) + (i >= 3 * K8), r = i - m * K8;
+        const uint32_t c = r >> 3, e = r & 7;  // chunk, eighth of the chunk
+        const uint32_t b = e >> 2, q = (e >> 1) & 1, half = e & 1;
+        unsigned char *base = lds + (m * 8 + b * 4) * DOT_PLANE + c * 16 + half * 8;
+        *(vkf_u2 *)(base + q * DOT_PLANE) = vkf_u2{hw[0], hw[1]};
+        *(vkf_u2 *)(base + (2 + q) * DOT_PLANE) = vkf_u2{lw[0], lw[1]};
+        if (e == 0)
+            *(vkf_i4 *)(lds + xs_offset<MM>(m, c)) =
+                vkf_i4{__float_as_int(__builtin_amdgcn_ldexpf(1.0f, E)), sum, s1, 0};
+    }
+}
+
+// P of one 32-element group: w[i] holds the codes of elements 4i..4i+3,
+// xb points at the chunk's entry in plane (m, b, 0).
+__device__ __forceinline__ int group_dot(const uint32_t w[8], const unsigned char *xb) {
+    const vkf_u4 h0 = *(const vkf_u4 *)xb, h1 = *(const vkf_u4 *)(xb + DOT_PLANE);
+    const vkf_u4 l0 = *(const vkf_u4 *)(xb + 2 * DOT_PLANE), l1 = *(const vkf_u4 *)(xb + 3 * DOT_PLANE);
     int ph = 0, pl = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -135,8 +151,9 @@ __device__ __forceinline__ int group_dot(const uint32_t w[8], const vkf_u4 *xq, 
 
 // ---------------------------------------------------------------------------
 // Formats.  Each chunk (64 elements, groups 2c and 2c+1 of a row) is loaded
-// as NW raw dwords, then decoded into integer codes w[2][8] plus per-group
-// constants, and finished by `fold` given P and the group's {2^E, fs}.
+// as NW raw dwords; `consts` extracts its scalars, `codes(raw, b, w)` the
+// integer codes of group b (w[i] = elements 4i..4i+3), and `fold` finishes
+// a group given P and the group's {2^E, fs}.
 // ---------------------------------------------------------------------------
 template <int QT> struct DotFmt;
 
@@ -150,7 +167,7 @@ __device__ __forceinline__ uint32_t nib_hi(uint32_t w) { return (w >> 4) & 0x0f0
 // A chunk = blocks 2c, 2c+1 = 36 bytes at a 4-byte aligned offset.
 template <> struct DotFmt<VKF_Q4_0> {
     static constexpr int NW = 9;
-    struct Dec { uint32_t w[2][8]; float d[2]; };
+    struct K { float d[2]; };
     static __device__ __forceinline__ void load(const uint8_t *row, uint32_t c, uint32_t r[NW]) {
         const uint8_t *p = row + 36ull * c;
         const vkf_u4 a = *(const vkf_u4a4 *)p, b = *(const vkf_u4a4 *)(p + 16);
@@ -158,20 +175,24 @@ template <> struct DotFmt<VKF_Q4_0> {
         r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
         r[8] = *(const uint32_t *)(p + 32);
     }
-    static __device__ __forceinline__ void decode(const uint32_t r[NW], uint32_t il, Dec &o) {
+    static __device__ __forceinline__ void consts(const uint32_t r[NW], uint32_t il, K &k) {
         (void)il;
-        o.d[0] = h_lo(r[0]);
-        o.d[1] = h_hi(r[4]);
+        k.d[0] = h_lo(r[0]);
+        k.d[1] = h_hi(r[4]);
+    }
+    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t w[8]) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t q0 = __builtin_amdgcn_alignbyte(r[i + 1], r[i], 2);  // bytes 2 + 4i ..
-            const uint32_t q1 = r[5 + i];                                         // bytes 20 + 4i ..
-            o.w[0][i] = nib_lo(q0); o.w[0][4 + i] = nib_hi(q0);
-            o.w[1][i] = nib_lo(q1); o.w[1][4 + i] = nib_hi(q1);
+            // block 0: qs at bytes 2..17, block 1: bytes 20..35
+            const uint32_t q = b == 0 ? __builtin_amdgcn_alignbyte(r[i + 1], r[i], 2) : r[5 + i];
+            w[i] = nib_lo(q);
+            w[4 + i] = nib_hi(q);
         }
     }
-    static __device__ __forceinline__ float fold(const Dec &o, int b, int P, float fe, float fs, float acc) {
-        return fmaf(o.d[b], fmaf(fe, (float)P, -8.0f * fs), acc);
+    // values (q - 8) * d: sum = d * 2^E * (P - 8*S) per block
+    static __device__ __forceinline__ float fold(const K &k, int P0, int P1, float fe, int S0, int S1, float acc) {
+        const float t = fmaf(k.d[1], (float)(P1 - 8 * S1), k.d[0] * (float)(P0 - 8 * S0));
+        return fmaf(fe, t, acc);
     }
 };
 
@@ -179,7 +200,7 @@ template <> struct DotFmt<VKF_Q4_0> {
 // = 40 bytes at an 8-byte aligned offset.
 template <> struct DotFmt<VKF_Q4_1> {
     static constexpr int NW = 10;
-    struct Dec { uint32_t w[2][8]; float d[2], m[2]; };
+    struct K { float d[2], m[2]; };
     static __device__ __forceinline__ void load(const uint8_t *row, uint32_t c, uint32_t r[NW]) {
         const uint8_t *p = row + 40ull * c;
         const vkf_u4 a = *(const vkf_u4a4 *)p, b = *(const vkf_u4a4 *)(p + 16);
@@ -188,22 +209,29 @@ template <> struct DotFmt<VKF_Q4_1> {
         r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
         r[8] = e[0]; r[9] = e[1];
     }
-    static __device__ __forceinline__ void decode(const uint32_t r[NW], uint32_t il, Dec &o) {
+    static __device__ __forceinline__ void consts(const uint32_t r[NW], uint32_t il, K &k) {
         (void)il;
 #pragma unroll
         for (int b = 0; b < 2; b++) {
-            o.d[b] = h_lo(r[5 * b]);
-            o.m[b] = h_hi(r[5 * b]);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t q = r[5 * b + 1 + i];
-                o.w[b][i] = nib_lo(q);
-                o.w[b][4 + i] = nib_hi(q);
-            }
+            k.d[b] = h_lo(r[5 * b]);
+            k.m[b] = h_hi(r[5 * b]);
         }
     }
-    static __device__ __forceinline__ float fold(const Dec &o, int b, int P, float fe, float fs, float acc) {
-        return fmaf(o.m[b], fs, fmaf(o.d[b], fe * (float)P, acc));
+    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t w[8]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t q = r[5 * b + 1 + i];
+            w[i] = nib_lo(q);
+            w[4 + i] = nib_hi(q);
+        }
+    }
+    // values q*d + m: sum = 2^E * (d*P + m*S) per block
+    static __device__ __forceinline__ float fold(const K &k, int P0, int P1, float fe, int S0, int S1, float acc) {
+        float t = k.d[0] * (float)P0;
+        t = fmaf(k.m[0], (float)S0, t);
+        t = fmaf(k.d[1], (float)P1, t);
+        t = fmaf(k.m[1], (float)S1, t);
+        return fmaf(fe, t, acc);
     }
 };
 
@@ -211,7 +239,7 @@ template <> struct DotFmt<VKF_Q4_1> {
 // 68 bytes at a 4-byte aligned offset.
 template <> struct DotFmt<VKF_Q8_0> {
     static constexpr int NW = 17;
-    struct Dec { uint32_t w[2][8]; float d[2]; };
+    struct K { float d[2]; };
     static __device__ __forceinline__ void load(const uint8_t *row, uint32_t c, uint32_t r[NW]) {
         const uint8_t *p = row + 68ull * c;
 #pragma unroll
@@ -221,19 +249,21 @@ template <> struct DotFmt<VKF_Q8_0> {
         }
         r[16] = *(const uint32_t *)(p + 64);
     }
-    static __device__ __forceinline__ void decode(const uint32_t r[NW], uint32_t il, Dec &o) {
+    static __device__ __forceinline__ void consts(const uint32_t r[NW], uint32_t il, K &k) {
         (void)il;
-        o.d[0] = h_lo(r[0]);
-        o.d[1] = h_hi(r[8]);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            o.w[0][i] = __builtin_amdgcn_alignbyte(r[i + 1], r[i], 2);  // bytes 2 + 4i ..
-            o.w[1][i] = r[9 + i];                                         // bytes 36 + 4i ..
-        }
+        k.d[0] = h_lo(r[0]);
+        k.d[1] = h_hi(r[8]);
     }
-    static __device__ __forceinline__ float fold(const Dec &o, int b, int P, float fe, float fs, float acc) {
-        (void)fs;
-        return fmaf(o.d[b], fe * (float)P, acc);
+    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t w[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)  // block 0: qs at bytes 2..33, block 1: bytes 36..67
+            w[i] = b == 0 ? __builtin_amdgcn_alignbyte(r[i + 1], r[i], 2) : r[9 + i];
+    }
+    // values q*d: sum = 2^E * d * P per block
+    static __device__ __forceinline__ float fold(const K &k, int P0, int P1, float fe, int S0, int S1, float acc) {
+        (void)S0;
+        (void)S1;
+        return fmaf(fe, fmaf(k.d[1], (float)P1, k.d[0] * (float)P0), acc);
     }
 };
 
@@ -246,54 +276,56 @@ template <> struct DotFmt<VKF_Q8_0> {
 // mn = (s[j+4] >> 4) | (s[j] >> 6) << 4.
 template <> struct DotFmt<VKF_Q4_K> {
     static constexpr int NW = 12;
-    struct Dec { uint32_t w[2][8]; float dall, dmin; int sc[2]; float mn[2]; };
+    struct K { float dall, dmin; int sc[2], mn[2]; };
     static __device__ __forceinline__ void load(const uint8_t *row, uint32_t c, uint32_t r[NW]) {
-        const uint8_t *p = row + 144ull * (c >> 2);
-        const vkf_u4 h = *(const vkf_u4 *)p;
-        const vkf_u4 a = *(const vkf_u4 *)(p + 16 + 32 * (c & 3)), b = *(const vkf_u4 *)(p + 32 + 32 * (c & 3));
+        const uint8_t *p = row + (144u * (c >> 2) + 32u * (c & 3));
+        const vkf_u4 h = *(const vkf_u4 *)(p - 32u * (c & 3));
+        const vkf_u4 a = *(const vkf_u4 *)(p + 16), b = *(const vkf_u4 *)(p + 32);
         r[0] = h[0]; r[1] = h[1]; r[2] = h[2]; r[3] = h[3];
         r[4] = a[0]; r[5] = a[1]; r[6] = a[2]; r[7] = a[3];
         r[8] = b[0]; r[9] = b[1]; r[10] = b[2]; r[11] = b[3];
     }
-    static __device__ __forceinline__ void decode(const uint32_t r[NW], uint32_t il, Dec &o) {
-        o.dall = h_lo(r[0]);
-        o.dmin = h_hi(r[0]);
+    static __device__ __forceinline__ void consts(const uint32_t r[NW], uint32_t il, K &k) {
+        k.dall = h_lo(r[0]);
+        k.dmin = h_hi(r[0]);
         const uint32_t s0 = r[1], s4 = r[2], s8 = r[3];
         // bytes k = 0..3 of scW / mnW: sc / mn of sub-block k (il < 2) or k + 4
         const uint32_t scW = il < 2 ? (s0 & 0x3f3f3f3fu) : ((s8 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u));
         const uint32_t mnW = il < 2 ? (s4 & 0x3f3f3f3fu) : (((s8 >> 4) & 0x0f0f0f0fu) | ((s4 >> 2) & 0x30303030u));
         const uint32_t sh = 16 * (il & 1);
-        o.sc[0] = (int)((scW >> sh) & 0xffu);
-        o.sc[1] = (int)((scW >> (sh + 8)) & 0xffu);
-        o.mn[0] = (float)((mnW >> sh) & 0xffu);
-        o.mn[1] = (float)((mnW >> (sh + 8)) & 0xffu);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            o.w[0][i] = nib_lo(r[4 + i]);
-            o.w[1][i] = nib_hi(r[4 + i]);
-        }
+        k.sc[0] = (int)((scW >> sh) & 0xffu);
+        k.sc[1] = (int)((scW >> (sh + 8)) & 0xffu);
+        k.mn[0] = (int)((mnW >> sh) & 0xffu);
+        k.mn[1] = (int)((mnW >> (sh + 8)) & 0xffu);
     }
-    static __device__ __forceinline__ float fold(const Dec &o, int b, int P, float fe, float fs, float acc) {
-        // sc * P: |P| < 2^22, sc < 64 -> exact in int32
-        return fmaf(-o.dmin, o.mn[b] * fs, fmaf(o.dall, fe * (float)(o.sc[b] * P), acc));
+    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t w[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = b == 0 ? nib_lo(r[4 + i]) : nib_hi(r[4 + i]);
+    }
+    // values dall*sc*q - dmin*mn: sum = 2^E * (dall*Q - dmin*mS) with the
+    // integers Q = sc0*P0 + sc1*P1 (|Q| < 2^29) and mS = mn0*S0 + mn1*S1
+    // (|mS| < 2^25), all factors within the 24-bit multiplier's range.
+    static __device__ __forceinline__ float fold(const K &k, int P0, int P1, float fe, int S0, int S1, float acc) {
+        const int Q = __mul24(k.sc[0], P0) + __mul24(k.sc[1], P1);
+        const int mS = __mul24(k.mn[0], S0) + __mul24(k.mn[1], S1);
+        return fmaf(fe, fmaf(k.dall, (float)Q, -k.dmin * (float)mS), acc);
     }
 };
 
 // ---------------------------------------------------------------------------
 // The kernel.  flags bit 0: y += instead of y =; bits 8..15: S (lanes per
-// row segment, a power of two 8..64).  Dynamic LDS: M*K*2 bytes of xq plus
-// M*K/4 bytes of xs.
+// row segment, a power of two 8..64).  Dynamic LDS: dot_lds_bytes<MM>().
+//
+// Each lane keeps the loads of its next D chunks in flight (a register ring
+// refilled as chunks are consumed); the first tile's loads are issued before
+// the activations are staged and each next tile's before the reduction.
 // ---------------------------------------------------------------------------
-template <int QT, int XK, int MM, int RPL>
+template <int QT, int XK, int MM, int RPL, int D>
 __device__ __forceinline__ void gemv_dot(const VkfGemvArgs &a) {
     using F = DotFmt<QT>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const uint32_t G = a.K / 32, C = G / 2;
     const uint32_t M = a.M;
-    vkf_u4 *xq = (vkf_u4 *)smem;
-    vkf_f4 *xs = (vkf_f4 *)(smem + (uint64_t)M * G * 64);
-    dot_stage_x<XK>(a, xq, xs, G, M);
-    __syncthreads();
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t S = (a.flags >> 8) & 0xffu;
@@ -302,55 +334,102 @@ __device__ __forceinline__ void gemv_dot(const VkfGemvArgs &a) {
     const uint32_t ntiles = (a.N + TR - 1) / TR;
     const uint32_t iters = (C + S - 1) / S;
     const uint32_t il = p & 3;  // Q4_K: chunk c = p + S*it has c & 3 == p & 3 (S % 4 == 0)
+    const uint32_t tstep = gridDim.x * DOT_WAVES;
 
-    for (uint32_t tile = wave * gridDim.x + blockIdx.x; tile < ntiles; tile += gridDim.x * DOT_WAVES) {
-        uint32_t n[RPL];
-        const uint8_t *row[RPL];
+    uint32_t n[RPL];
+    const uint8_t *row[RPL];
+    uint32_t raw[D][RPL][F::NW];
+    auto start_tile = [&](uint32_t tile) {
 #pragma unroll
         for (int j = 0; j < RPL; j++) {
             n[j] = tile * TR + seg * RPL + j;
             row[j] = a.w + (uint64_t)(n[j] < a.N ? n[j] : 0) * a.row_bytes;
         }
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const uint32_t c = p + d * S;
+            const uint32_t cl = c < C ? c : C - 1;  // clamped: every load in bounds
+#pragma unroll
+            for (int j = 0; j < RPL; j++) F::load(row[j], cl, raw[d][j]);
+        }
+    };
+
+    // Activations first: the first two staging rounds are loaded and
+    // quantised before any weight load is issued (a weight flood from the
+    // whole GPU ahead of them would delay every workgroup's staging), then
+    // the first tile's weights are requested while the rest is staged.
+    // (Waves whose first item of a round is past the end skip the round.)
+    const uint32_t K8 = a.K / 8, items = M * K8, w0 = wave * 64;
+    float xv[2][8];
+    dot_load_x<XK>(a, threadIdx.x, items, K8, xv[0]);
+    dot_load_x<XK>(a, blockDim.x + threadIdx.x, items, K8, xv[1]);
+    if (w0 < items) dot_store_x<MM>(smem, threadIdx.x, items, K8, xv[0]);
+    if (blockDim.x + w0 < items) dot_store_x<MM>(smem, blockDim.x + threadIdx.x, items, K8, xv[1]);
+    asm volatile("" ::: "memory");  // keep the weight loads below
+    uint32_t tile = wave * gridDim.x + blockIdx.x;
+    if (tile < ntiles) start_tile(tile);
+    for (uint32_t i0 = 2 * blockDim.x; i0 + w0 < items; i0 += blockDim.x) {
+        dot_load_x<XK>(a, i0 + threadIdx.x, items, K8, xv[0]);
+        dot_store_x<MM>(smem, i0 + threadIdx.x, items, K8, xv[0]);
+    }
+    __syncthreads();
+
+    for (; tile < ntiles; tile += tstep) {
         float acc[RPL][MM];
 #pragma unroll
         for (int j = 0; j < RPL; j++)
 #pragma unroll
             for (int m = 0; m < MM; m++) acc[j][m] = 0.0f;
 
-        // Loads of chunk it+1 are issued before chunk it is consumed.
-        uint32_t raw[RPL][F::NW];
-        {
-            const uint32_t c0 = p < C ? p : C - 1;
+        for (uint32_t it0 = 0; it0 < iters; it0 += D) {
 #pragma unroll
-            for (int j = 0; j < RPL; j++) F::load(row[j], c0, raw[j]);
-        }
-        for (uint32_t it = 0; it < iters; it++) {
-            const uint32_t c = p + it * S;
-            typename F::Dec dec[RPL];
+            for (int d = 0; d < D; d++) {
+                const uint32_t it = it0 + d;
+                if (it < iters) {
+                    const uint32_t c = p + it * S;
+                    if (c < C) {
+                        typename F::K k[RPL];
 #pragma unroll
-            for (int j = 0; j < RPL; j++) F::decode(raw[j], il, dec[j]);
-            if (it + 1 < iters) {
-                const uint32_t cn = c + S < C ? c + S : C - 1;
-#pragma unroll
-                for (int j = 0; j < RPL; j++) F::load(row[j], cn, raw[j]);
-            }
-            if (c < C) {
-#pragma unroll
-                for (int m = 0; m < MM; m++) {
-                    if (m < (int)M) {
-                        const vkf_f4 s = xs[(uint64_t)m * C + c];
+                        for (int j = 0; j < RPL; j++) F::consts(raw[d][j], il, k[j]);
+                        int P[2][RPL][MM];
 #pragma unroll
                         for (int b = 0; b < 2; b++) {
+                            uint32_t w[RPL][8];
 #pragma unroll
-                            for (int j = 0; j < RPL; j++) {
-                                const int P = group_dot(dec[j].w[b], xq, m, b, C, c);
-                                acc[j][m] = F::fold(dec[j], b, P, s[2 * b], s[2 * b + 1], acc[j][m]);
+                            for (int j = 0; j < RPL; j++) F::codes(raw[d][j], b, w[j]);
+#pragma unroll
+                            for (int m = 0; m < MM; m++) {
+                                if (MM == 1 || m < (int)M) {
+                                    const unsigned char *xb = smem + (m * 8 + b * 4) * DOT_PLANE + c * 16;
+#pragma unroll
+                                    for (int j = 0; j < RPL; j++) P[b][j][m] = group_dot(w[j], xb);
+                                }
                             }
                         }
+#pragma unroll
+                        for (int m = 0; m < MM; m++) {
+                            if (MM == 1 || m < (int)M) {
+                                const vkf_i4 xs = *(const vkf_i4 *)(smem + xs_offset<MM>(m, c));
+                                const float fe = __int_as_float(xs[0]);
+#pragma unroll
+                                for (int j = 0; j < RPL; j++)
+                                    acc[j][m] = F::fold(k[j], P[0][j][m], P[1][j][m], fe, xs[1], xs[2], acc[j][m]);
+                            }
+                        }
+                    }
+                    if (it + D < iters) {  // refill this slot with chunk it + D
+                        const uint32_t cn = c + D * S < C ? c + D * S : C - 1;
+#pragma unroll
+                        for (int j = 0; j < RPL; j++) F::load(row[j], cn, raw[d][j]);
                     }
                 }
             }
         }
+
+        uint32_t nout[RPL];
+#pragma unroll
+        for (int j = 0; j < RPL; j++) nout[j] = n[j];
+        if (tile + tstep < ntiles) start_tile(tile + tstep);  // next tile's loads under the reduction
 
         // segment reduction (segments are aligned groups of S lanes)
 #pragma unroll
@@ -359,8 +438,8 @@ __device__ __forceinline__ void gemv_dot(const VkfGemvArgs &a) {
             for (int m = 0; m < MM; m++) {
                 float v = acc[j][m];
                 for (uint32_t o = S >> 1; o > 0; o >>= 1) v += __shfl_xor(v, (int)o, 64);
-                if (p == 0 && m < (int)M && n[j] < a.N) {
-                    float *yp = a.y + (uint64_t)m * a.ldy + n[j];
+                if (p == 0 && m < (int)M && nout[j] < a.N) {
+                    float *yp = a.y + (uint64_t)m * a.ldy + nout[j];
                     *yp = (a.flags & 1u) ? *yp + v : v;
                 }
             }
@@ -368,19 +447,23 @@ __device__ __forceinline__ void gemv_dot(const VkfGemvArgs &a) {
     }
 }
 
+// Chunks kept in flight per lane: two (one consumed while the other loads)
+// for one row per lane, one for two rows.
+template <int QT> constexpr int dot_depth(int rpl) { return rpl == 1 ? 2 : 1; }
+
 // Kernel names: vkf_gemv_dot_{q4_0,q4_1,q8_0,q4_k}_{f16,f32}_m{1,4}.
 #define VKF_GEMV_DOT(name, QT)                                                                          \
     VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dot_##name##_f16_m1(VkfGemvArgs a) {     \
-        gemv_dot<QT, 0, 1, 1>(a);                                                                       \
+        gemv_dot<QT, 0, 1, 1, dot_depth<QT>(1)>(a);                                                                       \
     }                                                                                                   \
     VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dot_##name##_f32_m1(VkfGemvArgs a) {     \
-        gemv_dot<QT, 1, 1, 1>(a);                                                                       \
+        gemv_dot<QT, 1, 1, 1, dot_depth<QT>(1)>(a);                                                                       \
     }                                                                                                   \
     VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dot_##name##_f16_m4(VkfGemvArgs a) {     \
-        gemv_dot<QT, 0, 4, 2>(a);                                                                       \
+        gemv_dot<QT, 0, 4, 2, dot_depth<QT>(2)>(a);                                                                       \
     }                                                                                                   \
     VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dot_##name##_f32_m4(VkfGemvArgs a) {     \
-        gemv_dot<QT, 1, 4, 2>(a);                                                                       \
+        gemv_dot<QT, 1, 4, 2, dot_depth<QT>(2)>(a);                                                                       \
     }
 
 VKF_GEMV_DOT(q4_0, VKF_Q4_0)
