@@ -30,6 +30,7 @@
 
 #define BM 128
 #define BN 128
+#define PF 40  // fp16 LDS pitch of the Q6_K x Q8_1 kernel (32 k + 8 pad)
 
 __device__ __forceinline__ void epi_store(const VkfGemmArgs &a, uint32_t r, uint32_t c, float v) {
     if (a.rs) v *= a.rs[(a.flags & VKF_GF_RS_SCALAR) ? 0 : r];
@@ -52,87 +53,282 @@ __device__ __forceinline__ void epi_store(const VkfGemmArgs &a, uint32_t r, uint
 }
 
 // ---------------------------------------------------------------------------
-// fp16 operand tiles: 128 rows x 32 k, LDS row pitch 40 halves (80 B) so the
-// 16 rows read by one ds_read_b128 fall in distinct banks.
+// Pipelined core shared by the fp16, int8 and quantised-weight kernels.
+//
+// Each K step moves 128 bytes of K per operand row (64 fp16 or 128 int8
+// elements) into one of two LDS buffers (row pitch GP = 160 bytes: 16-byte
+// fragment reads of 16 consecutive rows spread over the banks).  Step kt+2
+// is loaded into registers while step kt is multiplied out of LDS[kt & 1]
+// and step kt+1 is written to the other buffer: one barrier per step, 32
+// MFMAs per wave between barriers.
 // ---------------------------------------------------------------------------
-#define KF 32
-#define PF 40
+#define GK 128  // bytes of K per step and operand row
+#define GP 160  // LDS row pitch (bytes)
 
-// Load one 128 x 32 fp16 tile into two 8-half registers per thread.
-// Thread t covers (row, 8-wide k chunk) for idx = t and t + 256.
-__device__ __forceinline__ void load_f16_tile(const _Float16 *P, uint64_t ld, bool trans, uint32_t nrows,
-                                              uint32_t row0, uint32_t K, uint32_t k0, vkf_h8 v[2]) {
+struct TileRegs {
+    vkf_i4 v[4];
+};
+
+// Dense operand tile: 128 rows x GK bytes of elements of ES bytes.  Thread t
+// covers rows t/8 + 32p (p < 4), bytes 16*(t%8) .. +15 of the step.
+template <int ES>
+__device__ __forceinline__ void load_dense(const void *P, uint64_t ld, bool trans, bool fast, uint32_t nrows,
+                                           uint32_t row0, uint32_t K, uint32_t k0, TileRegs &t) {
+    constexpr int EPC = 16 / ES;  // elements per 16-byte piece
+    const uint32_t k = k0 + EPC * (threadIdx.x & 7);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        int idx = threadIdx.x + 256 * i;
-        uint32_t r = row0 + (idx >> 2), k = k0 + 8 * (idx & 3);
-        vkf_h8 t = {};
+    for (int p = 0; p < 4; p++) {
+        const uint32_t r = row0 + (threadIdx.x >> 3) + 32 * p;
+        vkf_i4 v = {0, 0, 0, 0};
         if (r < nrows) {
-            if (!trans && k + 8 <= K && ((ld & 7) == 0) && (((uintptr_t)P & 15) == 0)) {
-                t = *(const vkf_h8 *)(P + (uint64_t)r * ld + k);
+            if (fast && k + EPC <= K) {
+                v = *(const vkf_i4 *)((const uint8_t *)P + ((uint64_t)r * ld + k) * ES);
             } else {
+                uint8_t bytes[16];
 #pragma unroll
-                for (int j = 0; j < 8; j++)
-                    if (k + j < K)
-                        t[j] = trans ? P[(uint64_t)(k + j) * ld + r] : P[(uint64_t)r * ld + k + j];
+                for (int e = 0; e < EPC; e++) {
+                    const uint64_t idx = trans ? (uint64_t)(k + e) * ld + r : (uint64_t)r * ld + k + e;
+                    const bool in = k + e < K;
+#pragma unroll
+                    for (int q = 0; q < ES; q++) bytes[e * ES + q] = in ? ((const uint8_t *)P)[idx * ES + q] : 0;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    v[j] = (int)((uint32_t)bytes[4 * j] | ((uint32_t)bytes[4 * j + 1] << 8) |
+                                 ((uint32_t)bytes[4 * j + 2] << 16) | ((uint32_t)bytes[4 * j + 3] << 24));
             }
         }
-        v[i] = t;
+        t.v[p] = v;
     }
 }
 
-__device__ __forceinline__ void store_f16_tile(_Float16 *lds, const vkf_h8 v[2]) {
+__device__ __forceinline__ void store_dense(uint8_t *lds, const TileRegs &t) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        int idx = threadIdx.x + 256 * i;
-        *(vkf_h8 *)(lds + (idx >> 2) * PF + 8 * (idx & 3)) = v[i];
-    }
+    for (int p = 0; p < 4; p++)
+        *(vkf_i4 *)(lds + ((threadIdx.x >> 3) + 32 * p) * GP + 16 * (threadIdx.x & 7)) = t.v[p];
 }
 
-// Dequantise a 128-row x 32-k tile of ggml weights to fp16.  Thread t covers
-// row t/2, elements 16*(t&1) .. +15 of the 32-element chunk k0/32.
+// Quantised operand tile dequantised to fp16: 128 rows x 64 k.  Thread t
+// covers row t/2, 32-element chunk k0/32 + (t&1): the reference's exact fp32
+// values (decode8) rounded to fp16.  Chunks at or past K are zero.
 template <int QT>
-__device__ __forceinline__ void load_q_tile(const uint8_t *W, uint64_t row_bytes, uint32_t nrows,
-                                            uint32_t row0, uint32_t k0, vkf_h8 v[2]) {
+__device__ __forceinline__ void load_quant(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                           uint32_t K, uint32_t k0, TileRegs &t) {
     constexpr int BB = QTraits<QT>::BB, CPB = QTraits<QT>::BE / 32;
-    uint32_t r = row0 + (threadIdx.x >> 1);
-    int h = threadIdx.x & 1;
-    v[0] = vkf_h8{};
-    v[1] = vkf_h8{};
-    if (r < nrows) {
-        uint32_t ch = k0 / 32, ib = ch / CPB, sub = ch - ib * CPB;
+    const uint32_t r = row0 + (threadIdx.x >> 1), kc = k0 + 32 * (threadIdx.x & 1);
+#pragma unroll
+    for (int g = 0; g < 4; g++) t.v[g] = vkf_i4{0, 0, 0, 0};
+    if (r < nrows && kc < K) {
+        const uint32_t ch = kc / 32, ib = ch / CPB, sub = ch - ib * CPB;
         const uint8_t *blk = W + (uint64_t)r * row_bytes + (uint64_t)ib * BB;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int g = 0; g < 4; g++) {
             float y[8];
-            decode8<QT>(blk, sub * 4 + 2 * h + i, y);
+            decode8<QT>(blk, sub * 4 + g, y);
+            vkf_h8 h;
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[i][j] = vkf_to_f16(y[j]);
+            for (int j = 0; j < 8; j++) h[j] = vkf_to_f16(y[j]);
+            t.v[g] = __builtin_bit_cast(vkf_i4, h);
         }
     }
 }
 
-__device__ __forceinline__ void store_q_tile(_Float16 *lds, const vkf_h8 v[2]) {
-    int row = threadIdx.x >> 1, h = threadIdx.x & 1;
-    *(vkf_h8 *)(lds + row * PF + 16 * h) = v[0];
-    *(vkf_h8 *)(lds + row * PF + 16 * h + 8) = v[1];
+__device__ __forceinline__ void store_quant(uint8_t *lds, const TileRegs &t) {
+    uint8_t *p = lds + (threadIdx.x >> 1) * GP + 64 * (threadIdx.x & 1);
+#pragma unroll
+    for (int g = 0; g < 4; g++) *(vkf_i4 *)(p + 16 * g) = t.v[g];
 }
 
-// One 32-deep step of the 64x64 wave tile.
-__device__ __forceinline__ void mfma_step_f16(const _Float16 *ax, const _Float16 *ay, int wr, int wc,
-                                              vkf_f4 acc[4][4]) {
+// Operand sources: dense fp16 / int8 or quantised blocks (QT >= 0).
+template <int ES, int QT>
+struct Operand {
+    const void *P;
+    uint64_t ld;  // elements (dense) or bytes per row (quantised)
+    bool trans, fast;
+    uint32_t nrows, row0, K;
+    __device__ __forceinline__ void load(uint32_t kt, TileRegs &t) const {
+        if constexpr (QT >= 0) load_quant<QT>((const uint8_t *)P, ld, nrows, row0, K, kt * (GK / 2), t);
+        else load_dense<ES>(P, ld, trans, fast, nrows, row0, K, kt * (GK / ES), t);
+    }
+    __device__ __forceinline__ void store(uint8_t *lds, const TileRegs &t) const {
+        if constexpr (QT >= 0) store_quant(lds, t);
+        else store_dense(lds, t);
+    }
+};
+
+template <int ES, int QT>
+__device__ __forceinline__ Operand<ES, QT> make_operand(const void *P, uint64_t ld, bool trans, uint32_t nrows,
+                                                        uint32_t row0, uint32_t K) {
+    Operand<ES, QT> o;
+    o.P = P;
+    o.ld = ld;
+    o.trans = trans;
+    o.fast = !trans && ((ld * ES) % 16) == 0 && (((uintptr_t)P & 15) == 0);
+    o.nrows = nrows;
+    o.row0 = row0;
+    o.K = K;
+    return o;
+}
+
+// One K step of the wave's 64x64 tile from LDS: two 16x16x32 fp16 MFMAs or
+// two 16x16x64 int8 MFMAs deep per 16x16 sub-tile.
+template <int ES, class ACC>
+__device__ __forceinline__ void mfma_step(const uint8_t *lx, const uint8_t *ly, int wr, int wc, ACC acc[4][4]) {
     const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
-    vkf_h8 fa[4], fb[4];
+    // all 16 fragments first: the second slice's reads overlap the first
+    // slice's MFMAs (LDS results return in issue order)
+    vkf_i4 fa[2][4], fb[2][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) fa[i] = *(const vkf_h8 *)(ax + (wr * 64 + 16 * i + li) * PF + 8 * lg);
+    for (int s = 0; s < 2; s++) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) fb[j] = *(const vkf_h8 *)(ay + (wc * 64 + 16 * j + li) * PF + 8 * lg);
+        for (int i = 0; i < 4; i++)
+            fa[s][i] = *(const vkf_i4 *)(lx + (wr * 64 + 16 * i + li) * GP + 64 * s + 16 * lg);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            fb[s][j] = *(const vkf_i4 *)(ly + (wc * 64 + 16 * j + li) * GP + 64 * s + 16 * lg);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if constexpr (ES == 2)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vkf_h8, fa[s][i]),
+                                                                       __builtin_bit_cast(vkf_h8, fb[s][j]),
+                                                                       acc[i][j], 0, 0, 0);
+                else
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
+            }
+}
+
+// The pipelined K loop: acc += X[r0.., :] . Y[c0.., :]^T.  The loads of the
+// next GNS steps are in flight in a ring of register sets while the current
+// step is multiplied out of LDS.  smem: GEMM_LDS bytes (two buffers per
+// operand).
+#define GNS 2
+#define GEMM_LDS (4 * 128 * GP)
+// 256 threads, at most 256 registers per lane (two waves per SIMD).
+#define GEMM_KERNEL VKF_KERNEL void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+template <int ES, class OX, class OY, class ACC>
+__device__ __forceinline__ void gemm_mainloop(const OX &ox, const OY &oy, uint32_t K, uint32_t kelem_per_step,
+                                              ACC acc[4][4], uint8_t *smem) {
+    uint8_t *lx[2] = {smem, smem + 128 * GP}, *ly[2] = {smem + 2 * 128 * GP, smem + 3 * 128 * GP};
+    const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
+    const uint32_t nk = (K + kelem_per_step - 1) / kelem_per_step;
+    TileRegs rx[GNS], ry[GNS];
+#pragma unroll
+    for (int u = 0; u < GNS; u++) {
+        if ((uint32_t)u < nk) {
+            ox.load(u, rx[u]);
+            oy.load(u, ry[u]);
+        }
+    }
+    ox.store(lx[0], rx[0]);
+    oy.store(ly[0], ry[0]);
+    if (GNS < nk) {
+        ox.load(GNS, rx[0]);
+        oy.load(GNS, ry[0]);
+    }
+    __syncthreads();
+    for (uint32_t kt0 = 0; kt0 < nk; kt0 += GNS) {
+#pragma unroll
+        for (int u = 0; u < GNS; u++) {  // GNS even: LDS parity = u & 1
+            const uint32_t kt = kt0 + u;
+            if (kt < nk) {
+                mfma_step<ES>(lx[u & 1], ly[u & 1], wr, wc, acc);
+                const int nslot = (u + 1) % GNS;
+                if (kt + 1 < nk) {
+                    ox.store(lx[(u + 1) & 1], rx[nslot]);
+                    oy.store(ly[(u + 1) & 1], ry[nslot]);
+                }
+                if (kt + 1 + GNS < nk) {
+                    ox.load(kt + 1 + GNS, rx[nslot]);
+                    oy.load(kt + 1 + GNS, ry[nslot]);
+                }
+                __syncthreads();
+            }
+        }
+    }
+}
+
+// Float epilogue (epi_store's arithmetic) of the workgroup's 128x128 tile:
+// each lane finishes its 64 values, the tile is staged as fp32 rows in LDS
+// (pitch 132 floats) and written out as 16-byte row vectors when D's rows
+// allow it, element by element otherwise.  smem must be free (the main loop
+// ends with a barrier).
+template <class ACC>
+__device__ __forceinline__ void epilogue_tile(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC acc[4][4],
+                                              uint8_t *smem) {
+    constexpr int TP = 132;
+    const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
+    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+    float *tile = (float *)smem;
+    float csv[4], bcv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t c = c0 + wc * 64 + 16 * j + li, cc = c < a.Cn ? c : a.Cn - 1;
+        csv[j] = a.cs ? a.cs[(a.flags & VKF_GF_CS_SCALAR) ? 0 : cc] : 1.0f;
+        bcv[j] = 0.0f;
+        if (a.bias && !(a.flags & VKF_GF_BIAS_ROW))
+            bcv[j] = (a.flags & VKF_GF_BIAS_F32) ? ((const float *)a.bias)[cc] : (float)((const _Float16 *)a.bias)[cc];
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        for (int e = 0; e < 4; e++) {
+            const int tr = wr * 64 + 16 * i + 4 * lg + e;
+            const uint32_t r = r0 + tr, rr = r < a.R ? r : a.R - 1;
+            const float rsv = a.rs ? a.rs[(a.flags & VKF_GF_RS_SCALAR) ? 0 : rr] : 1.0f;
+            float brv = 0.0f;
+            if (a.bias && (a.flags & VKF_GF_BIAS_ROW))
+                brv = (a.flags & VKF_GF_BIAS_F32) ? ((const float *)a.bias)[rr] : (float)((const _Float16 *)a.bias)[rr];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t c = c0 + wc * 64 + 16 * j + li;
+                float v = (float)acc[i][j][e];
+                if (a.rs) v *= rsv;
+                if (a.cs) v *= csv[j];
+                v *= a.alpha;
+                if (a.beta != 0.0f && r < a.R && c < a.Cn) {
+                    const float cin = (a.flags & VKF_GF_CIN_F32)
+                                          ? ((const float *)a.Cin)[(uint64_t)r * a.ldc + c]
+                                          : (float)((const _Float16 *)a.Cin)[(uint64_t)r * a.ldc + c];
+                    v = fmaf(a.beta, cin, v);
+                }
+                if (a.bias) v += (a.flags & VKF_GF_BIAS_ROW) ? brv : bcv[j];
+                tile[tr * TP + wc * 64 + 16 * j + li] = vkf_act(a.act, v);
+            }
+        }
+    __syncthreads();
+    const bool f32 = (a.flags & VKF_GF_D_F32) != 0;
+    const uint32_t vec = f32 ? 4 : 8;  // elements per 16-byte store
+    const bool vok = (a.ldd % vec) == 0 && (((uintptr_t)a.D & 15) == 0);
+    const uint32_t per_row = 128 / vec;
+    for (uint32_t q = threadIdx.x; q < 128 * per_row; q += 256) {
+        const uint32_t tr = q / per_row, tc = (q % per_row) * vec;
+        const uint32_t r = r0 + tr, c = c0 + tc;
+        if (r >= a.R || c >= a.Cn) continue;
+        const float *src = tile + tr * TP + tc;
+        if (vok && c + vec <= a.Cn) {
+            if (f32) {
+                *(vkf_f4 *)((float *)a.D + (uint64_t)r * a.ldd + c) = *(const vkf_f4 *)src;
+            } else {
+                vkf_h8 h;
+#pragma unroll
+                for (int k = 0; k < 8; k++) h[k] = vkf_to_f16(src[k]);
+                *(vkf_h8 *)((_Float16 *)a.D + (uint64_t)r * a.ldd + c) = h;
+            }
+        } else {
+            for (uint32_t k = 0; k < vec && c + k < a.Cn; k++) {
+                if (f32) ((float *)a.D)[(uint64_t)r * a.ldd + c + k] = src[k];
+                else ((_Float16 *)a.D)[(uint64_t)r * a.ldd + c + k] = vkf_to_f16(src[k]);
+            }
+        }
+    }
 }
 
+// Per-element epilogue (the Q6_K x Q8_1 kernel's LDS layout differs).
 __device__ __forceinline__ void store_acc_f32(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, int wr, int wc,
                                               vkf_f4 acc[4][4]) {
     const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
@@ -151,55 +347,24 @@ __device__ __forceinline__ void store_acc_f32(const VkfGemmArgs &a, uint32_t r0,
 // fp16(dx*q)).  QT < 0: dense fp16 Y; otherwise Y holds ggml blocks of type QT.
 template <int XQT, int QT>
 __device__ __forceinline__ void gemm_f16_body(const VkfGemmArgs &a) {
-    __shared__ __attribute__((aligned(16))) _Float16 lx[2][BM * PF];
-    __shared__ __attribute__((aligned(16))) _Float16 ly[2][BN * PF];
-    const uint32_t r0 = blockIdx.y * BM, c0 = blockIdx.x * BN;
-    const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
-    const bool xt = a.flags & VKF_GF_X_TRANS, yt = a.flags & VKF_GF_Y_TRANS;
+    const uint32_t r0 = blockIdx.y * 128, c0 = blockIdx.x * 128;
     vkf_f4 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
-
-    const uint32_t nk = (a.K + KF - 1) / KF;
-    vkf_h8 vx[2], vy[2];
-    if constexpr (XQT < 0) load_f16_tile((const _Float16 *)a.X, a.ldx, xt, a.R, r0, a.K, 0, vx);
-    else load_q_tile<XQT>((const uint8_t *)a.X, a.ldx, a.R, r0, 0, vx);
-    if constexpr (QT < 0) load_f16_tile((const _Float16 *)a.Y, a.ldy, yt, a.Cn, c0, a.K, 0, vy);
-    else load_q_tile<QT>((const uint8_t *)a.Y, a.ldy, a.Cn, c0, 0, vy);
-    if constexpr (XQT < 0) store_f16_tile(lx[0], vx);
-    else store_q_tile(lx[0], vx);
-    if constexpr (QT < 0) store_f16_tile(ly[0], vy);
-    else store_q_tile(ly[0], vy);
-    __syncthreads();
-    for (uint32_t kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) {
-            uint32_t k1 = (kt + 1) * KF;
-            if constexpr (XQT < 0) load_f16_tile((const _Float16 *)a.X, a.ldx, xt, a.R, r0, a.K, k1, vx);
-            else load_q_tile<XQT>((const uint8_t *)a.X, a.ldx, a.R, r0, k1, vx);
-            if constexpr (QT < 0) load_f16_tile((const _Float16 *)a.Y, a.ldy, yt, a.Cn, c0, a.K, k1, vy);
-            else load_q_tile<QT>((const uint8_t *)a.Y, a.ldy, a.Cn, c0, k1, vy);
-        }
-        mfma_step_f16(lx[cur], ly[cur], wr, wc, acc);
-        if (more) {
-            if constexpr (XQT < 0) store_f16_tile(lx[cur ^ 1], vx);
-            else store_q_tile(lx[cur ^ 1], vx);
-            if constexpr (QT < 0) store_f16_tile(ly[cur ^ 1], vy);
-            else store_q_tile(ly[cur ^ 1], vy);
-        }
-        __syncthreads();
-    }
-    store_acc_f32(a, r0, c0, wr, wc, acc);
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_LDS];
+    const auto ox = make_operand<2, XQT>(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.R, r0, a.K);
+    const auto oy = make_operand<2, QT>(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.Cn, c0, a.K);
+    gemm_mainloop<2>(ox, oy, a.K, 64, acc, smem);
+    epilogue_tile(a, r0, c0, acc, smem);
 }
 
-VKF_KERNEL void __launch_bounds__(256) vkf_gemm_f16(VkfGemmArgs a) { gemm_f16_body<-1, -1>(a); }
+GEMM_KERNEL vkf_gemm_f16(VkfGemmArgs a) { gemm_f16_body<-1, -1>(a); }
 #define VKF_GEMM_Q(name, QT)                                                                        \
-    VKF_KERNEL void __launch_bounds__(256) vkf_gemm_##name##_f16(VkfGemmArgs a) { gemm_f16_body<-1, QT>(a); }
+    GEMM_KERNEL vkf_gemm_##name##_f16(VkfGemmArgs a) { gemm_f16_body<-1, QT>(a); }
 #define VKF_GEMM_Q_Q81(name, QT)                                                                    \
-    VKF_KERNEL void __launch_bounds__(256) vkf_gemm_##name##_q8_1(VkfGemmArgs a) {                  \
+    GEMM_KERNEL vkf_gemm_##name##_q8_1(VkfGemmArgs a) {                                            \
         gemm_f16_body<VKF_Q8_1, QT>(a);                                                             \
     }
 VKF_GEMM_Q(q4_0, VKF_Q4_0)
@@ -218,106 +383,40 @@ VKF_GEMM_Q_Q81(q5_k, VKF_Q5_K)
 
 // ---------------------------------------------------------------------------
 // int8 x int8 -> int32 (kernels/linear_int8.glsl:54-93, with int8 A).
-// Tiles 128 x 64 int8, LDS pitch 80 B.  flags & VKF_GF_D_F32 selects the
-// float epilogue with fp32 D; VKF_GF_D_I32 stores the raw int32 accumulator.
+// flags & VKF_GF_D_F32 selects the float epilogue with fp32 D; VKF_GF_D_I32
+// stores the raw int32 accumulator.
 // ---------------------------------------------------------------------------
-#define KI 64
-#define PI 80
-
-__device__ __forceinline__ void load_i8_tile(const int8_t *P, uint64_t ld, bool trans, uint32_t nrows, uint32_t row0,
-                                             uint32_t K, uint32_t k0, vkf_i4 v[2]) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        int idx = threadIdx.x + 256 * i;
-        uint32_t r = row0 + (idx >> 2), k = k0 + 16 * (idx & 3);
-        vkf_i4 t = {0, 0, 0, 0};
-        if (r < nrows) {
-            if (!trans && k + 16 <= K && ((ld & 15) == 0) && (((uintptr_t)P & 15) == 0)) {
-                t = *(const vkf_i4 *)(P + (uint64_t)r * ld + k);
-            } else {
-                uint8_t bytes[16];
-#pragma unroll
-                for (int j = 0; j < 16; j++)
-                    bytes[j] = (k + j < K) ? (uint8_t)(trans ? P[(uint64_t)(k + j) * ld + r] : P[(uint64_t)r * ld + k + j]) : 0;
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    t[j] = (int)((uint32_t)bytes[4 * j] | ((uint32_t)bytes[4 * j + 1] << 8) |
-                                 ((uint32_t)bytes[4 * j + 2] << 16) | ((uint32_t)bytes[4 * j + 3] << 24));
-            }
-        }
-        v[i] = t;
-    }
-}
-
-__device__ __forceinline__ void store_i8_tile(int8_t *lds, const vkf_i4 v[2]) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        int idx = threadIdx.x + 256 * i;
-        *(vkf_i4 *)(lds + (idx >> 2) * PI + 16 * (idx & 3)) = v[i];
-    }
-}
-
-VKF_KERNEL void __launch_bounds__(256) vkf_gemm_i8(VkfGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t lx[2][BM * PI];
-    __shared__ __attribute__((aligned(16))) int8_t ly[2][BN * PI];
-    const uint32_t r0 = blockIdx.y * BM, c0 = blockIdx.x * BN;
-    const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
-    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
-    const bool xt = a.flags & VKF_GF_X_TRANS, yt = a.flags & VKF_GF_Y_TRANS;
+GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_LDS];
+    const uint32_t r0 = blockIdx.y * 128, c0 = blockIdx.x * 128;
     vkf_i4 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = vkf_i4{0, 0, 0, 0};
-    const uint32_t nk = (a.K + KI - 1) / KI;
-    vkf_i4 vx[2], vy[2];
-    load_i8_tile((const int8_t *)a.X, a.ldx, xt, a.R, r0, a.K, 0, vx);
-    load_i8_tile((const int8_t *)a.Y, a.ldy, yt, a.Cn, c0, a.K, 0, vy);
-    store_i8_tile(lx[0], vx);
-    store_i8_tile(ly[0], vy);
-    __syncthreads();
-    for (uint32_t kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) {
-            load_i8_tile((const int8_t *)a.X, a.ldx, xt, a.R, r0, a.K, (kt + 1) * KI, vx);
-            load_i8_tile((const int8_t *)a.Y, a.ldy, yt, a.Cn, c0, a.K, (kt + 1) * KI, vy);
-        }
-        vkf_i4 fa[4], fb[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) fa[i] = *(const vkf_i4 *)(lx[cur] + (wr * 64 + 16 * i + li) * PI + 16 * lg);
-#pragma unroll
-        for (int j = 0; j < 4; j++) fb[j] = *(const vkf_i4 *)(ly[cur] + (wc * 64 + 16 * j + li) * PI + 16 * lg);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-        if (more) {
-            store_i8_tile(lx[cur ^ 1], vx);
-            store_i8_tile(ly[cur ^ 1], vy);
-        }
-        __syncthreads();
+    const auto ox = make_operand<1, -1>(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.R, r0, a.K);
+    const auto oy = make_operand<1, -1>(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.Cn, c0, a.K);
+    gemm_mainloop<1>(ox, oy, a.K, 128, acc, smem);
+    if (!(a.flags & VKF_GF_D_I32)) {
+        epilogue_tile(a, r0, c0, acc, smem);
+        return;
     }
+    // raw int32 accumulator with integer alpha/beta (hipblasGemmEx, compute 32I)
+    const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
+    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+    const int32_t al = (int32_t)a.alpha, be = (int32_t)a.beta;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                uint32_t r = r0 + wr * 64 + 16 * i + 4 * lg + e, c = c0 + wc * 64 + 16 * j + li;
+                const uint32_t r = r0 + wr * 64 + 16 * i + 4 * lg + e, c = c0 + wc * 64 + 16 * j + li;
                 if (r < a.R && c < a.Cn) {
-                    if (a.flags & VKF_GF_D_I32) {
-                        int32_t *dp = (int32_t *)a.D + (uint64_t)r * a.ldd + c;
-                        int32_t v = acc[i][j][e];
-                        // integer alpha/beta (hipblasGemmEx with compute 32I)
-                        if (a.alpha != 1.0f || a.beta != 0.0f) {
-                            int32_t al = (int32_t)a.alpha, be = (int32_t)a.beta;
-                            v = al * v + (be ? be * ((const int32_t *)a.Cin)[(uint64_t)r * a.ldc + c] : 0);
-                        }
-                        *dp = v;
-                    } else {
-                        epi_store(a, r, c, (float)acc[i][j][e]);
-                    }
+                    int32_t v = acc[i][j][e];
+                    if (al != 1 || be != 0)
+                        v = al * v + (be ? be * ((const int32_t *)a.Cin)[(uint64_t)r * a.ldc + c] : 0);
+                    ((int32_t *)a.D)[(uint64_t)r * a.ldd + c] = v;
                 }
             }
 }
