@@ -191,8 +191,8 @@ def cpu_baseline(O, N, K, wbytes, seed):
     w = O.gen_weight(O.Q4_K, N, K, seed)
     x = np.random.default_rng(seed + 1).normal(0, 1, (1, K)).astype(np.float16).astype(np.float32)
     times = []
-    t_end = time.perf_counter() + 20.0
-    while len(times) < 5 and (len(times) < 2 or time.perf_counter() < t_end):
+    t_end = time.perf_counter() + 10.0  # ~10 s of CPU work, at least 3 runs
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 100):
         t0 = time.perf_counter()
         wd = O.np_dequant(O.Q4_K, w).reshape(N, K)
         _ = x @ wd.T
@@ -279,7 +279,7 @@ def main():
             traffic = json.load(f).get("hbm_bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "vkf_gemv_q4_k_f16", "algorithmic_bytes_per_launch": alg_bytes}
+                "kernel": "vkf_gemv_dot_q4_k_f16_m1", "algorithmic_bytes_per_launch": alg_bytes}
 
     suite = None if args.no_suite else run_suite(torch, ops, O, reps=20)
     cpu = None if args.no_cpu else cpu_baseline(O, N, K, wbytes, seed)

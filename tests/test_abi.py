@@ -30,6 +30,15 @@ def _declared():
     return sorted(set(re.findall(r"\b(vkflame_\w+)\s*\(", txt)))
 
 
+def _declared_blas():
+    txt = open(os.path.join(ROOT, "include", "vkflame_amd_blas.h")).read()
+    return sorted(set(re.findall(r"\bX\((hipblas\w+),", txt)))
+
+
+def test_blas_header_lists_the_exports():
+    assert _declared_blas() == sorted(HIPBLAS + HIPBLASLT)
+
+
 def _exported(path):
     out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
     return {l.split()[-1] for l in out.splitlines() if " T " in l}

@@ -7,19 +7,20 @@
 // the activations are turned into integers once per workgroup instead, and
 // each weight byte meets them in v_dot4_i32_i8 (4 MACs per instruction):
 //
-//   per 32-element group g of activation row m: E = exponent with
-//   max|x| < 2^(E+13), v = rint(x * 2^-E) in [-8192, 8192]
-//   (|x - v*2^E| <= 2^(E-1) <= max|x| / 16384), split exactly as
-//   v = 128*h + l with h in [-64, 64], l in [0, 127] (both int8).
+//   per 64-element chunk of activation row m (two 32-element groups):
+//   E = exponent with max|x| < 2^(E+13), v = rint(x * 2^-E) in
+//   [-8192, 8192] (|x - v*2^E| <= 2^(E-1) <= max|x| / 16384), split exactly
+//   as v = 128*h + l with h in [-64, 64], l in [0, 127] (both int8).
 //
 // For a 32-weight group with integer codes q (nibbles 0..15, or Q8_0's int8):
 //   P = 128 * sum(q*h) + sum(q*l) = sum(q*v)      exact, |P| < 2^22
 // and the group's output contribution is the format's affine map applied to
-// P and S = sum(v) (stored as fs = 2^E * S):
-//   Q4_0  d * (2^E*P - 8*fs)           (value (q - 8) * d)
-//   Q4_1  d * 2^E*P + m * fs           (value q*d + m)
-//   Q8_0  d * 2^E*P                    (value q*d)
-//   Q4_K  dall * 2^E*(sc*P) - dmin * mn * fs   (value dall*sc*q - dmin*mn)
+// P and the group's activation sum S = sum(v):
+//   Q4_0  2^E * d * (P - 8*S)          (value (q - 8) * d)
+//   Q4_1  2^E * (d*P + m*S)            (value q*d + m)
+//   Q8_0  2^E * d * P                  (value q*d)
+//   Q4_K  2^E * (dall*(sc*P) - dmin*(mn*S))   (value dall*sc*q - dmin*mn;
+//         the two groups of a chunk share E, so their integers add first)
 // The 14-bit activation grid is the only rounding besides fp32 accumulation:
 // it bounds the output error by ~1e-4 of max|y| (1e-3 tolerance).
 //
