@@ -183,3 +183,20 @@ def test_gemv_dot_dynamic_range(dev, qt):
     assert np.all(y[1] == 0.0)
     for m in (0, 2, 3):
         assert rel_err(y[m], ref[m]) <= TOL_F32, m
+
+
+@pytest.mark.parametrize("N", [1, 77, 3001])
+@pytest.mark.parametrize("K", [2048, 4608])
+def test_gemv_q6k_q81_dot(dev, N, K):
+    """The Q6_K x Q8_1 integer GEMV at M = 1 (4-byte aligned rows, chunks at
+    alternating 2- and 4-byte offsets), including scales over the whole int8
+    range."""
+    from vkflame_amd import ops
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(5, 10 + N % 7)).reshape(-1, 210)
+    rng = np.random.default_rng(seed_for(5, 11))
+    w[::3, 192:208] = rng.integers(-128, 128, (w[::3].shape[0], 16)).astype(np.int8).view(np.uint8)
+    w = w.reshape(N, -1)
+    xq, x64 = _x("q8_1", 1, K, seed_for(5, 12))
+    y = ops.gemm_q(to_dev(w, dev), O.Q6_K, to_dev(xq, dev), N, K).cpu().numpy()
+    ref = O.ref_gemv(x64, O.np_dequant(O.Q6_K, w).reshape(N, K))
+    assert rel_err(y, ref) <= TOL_F32

@@ -1,0 +1,190 @@
+// gemv_q6k.hip — decode GEMV of Q6_K weights x Q8_1 activations (a
+// vocabulary projection at decode), M = 1, integer dot products.
+//
+// y[m, n] = sum over 32-element blocks kb of dw(n, sb) * dx(m, kb) * Q,
+//   Q = sum_l sc * (u_l - 32) * q_l          (exact int32)
+// with u the 6-bit code (low nibble from ql, two high bits from qh), sc the
+// int8 sub-block scale (one per 16 elements) and q the Q8_1 activation
+// (kernels/dequant_q6_k.glsl:34-58 for the element order; the arithmetic is
+// ggml's vec_dot_q6_K_q8_1).  u*q runs in v_dot4_i32_i8; the -32 offset
+// is applied to the integer activation sums X = sum q of each 16-element half.
+//
+// Layout.  A chunk is one 128-element half of a super-block (ip = c & 1 of
+// super-block c >> 1): ql[64ip .. +63], qh[32ip .. +31], sc[8ip .. +7] and d,
+// 106 bytes for 128 weights.  Super-blocks are 210 bytes, so a chunk's
+// fields sit at a 2-byte (odd super-block) or 4-byte (even) offset from the
+// 4-byte aligned row start; each field is loaded as the aligned dwords that
+// cover it and realigned with v_alignbyte.
+//
+// Work split as in gemv_dot.hip: one 1024-thread workgroup per CU stages the
+// activations in LDS, segments of S lanes own rows, lane p takes chunks p,
+// p+S, ..., and the segment reduces with lane shuffles.  A chunk is ~27
+// dwords of loads; a second chunk in flight per lane does not fit the 128
+// registers of a 16-wave workgroup without spilling (measured slower), so
+// the 16 waves of a CU overlap each other's loads instead.
+#include "vkf_device.h"
+
+#define Q6_WAVES 16
+// bytes per LDS plane: 16 per chunk; MM = 1 up to 256 chunks (K <= 32768),
+// MM = 4 up to 128 (K <= 16384)
+template <int MM> constexpr uint32_t q6_plane_bytes() { return MM == 1 ? 4096 : 2048; }
+
+typedef unsigned int vkf_u4 __attribute__((ext_vector_type(4)));
+typedef unsigned int vkf_u4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// LDS image of MM activation rows, per chunk c (4 Q8_1 blocks t = 0..3):
+//   planes m*11 + j, j = 0..7: bytes 16j .. 16j+15 of the chunk's 128 q;
+//   plane m*11 + 8: {dx(t)} as 4 floats; planes 9, 10: {X0(t)}, {X1(t)}
+//   (sums of q over elements 0..15 and 16..31 of block t).
+template <int MM>
+__device__ __forceinline__ unsigned char *q6_plane(unsigned char *lds, uint32_t m, uint32_t j, uint32_t c) {
+    return lds + (m * 11 + j) * q6_plane_bytes<MM>() + c * 16;
+}
+
+// One thread per Q8_1 block: row m, block kb (36 bytes: fp16 d, fp16 s,
+// int8 q[32]; the s field is not used).
+template <int MM>
+__device__ __forceinline__ void q6_stage_block(const VkfGemvArgs &a, unsigned char *lds, uint32_t m, uint32_t kb) {
+    const uint32_t *b = (const uint32_t *)((const uint8_t *)a.x + (uint64_t)m * a.ldx + 36ull * kb);
+    uint32_t q[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = b[1 + i];
+    const float dx = vkf_h2f(b[0] & 0xffffu);
+    int x0 = 0, x1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        x0 = __builtin_amdgcn_sdot4((int)q[i], 0x01010101, x0, false);
+        x1 = __builtin_amdgcn_sdot4((int)q[4 + i], 0x01010101, x1, false);
+    }
+    const uint32_t c = kb >> 2, t = kb & 3;
+    *(vkf_u4 *)q6_plane<MM>(lds, m, 2 * t, c) = vkf_u4{q[0], q[1], q[2], q[3]};
+    *(vkf_u4 *)q6_plane<MM>(lds, m, 2 * t + 1, c) = vkf_u4{q[4], q[5], q[6], q[7]};
+    ((float *)q6_plane<MM>(lds, m, 8, c))[t] = dx;
+    ((int *)q6_plane<MM>(lds, m, 9, c))[t] = x0;
+    ((int *)q6_plane<MM>(lds, m, 10, c))[t] = x1;
+}
+
+// Raw dwords of one chunk: ql 17, qh 9, sc 3 (one extra dword each for the
+// realignment), and the fp16 d.  Every load stays inside the chunk's
+// super-block: the dwords beyond byte 209 that an even super-block would
+// need for sc are never needed (no realignment there) and d is a 2-byte load.
+struct Q6Raw {
+    uint32_t ql[17], qh[9], sc[3], d;
+};
+
+__device__ __forceinline__ void q6_load(const uint8_t *row, uint32_t c, Q6Raw &r) {
+    const uint32_t sb = c >> 1, ip = c & 1;
+    const uint32_t base = 210u * sb - 2u * (sb & 1);  // 4-byte aligned
+    const uint8_t *p = row + base;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const vkf_u4 v = *(const vkf_u4a4 *)(p + 64 * ip + 16 * k);
+        r.ql[4 * k] = v[0]; r.ql[4 * k + 1] = v[1]; r.ql[4 * k + 2] = v[2]; r.ql[4 * k + 3] = v[3];
+    }
+    r.ql[16] = *(const uint32_t *)(p + 64 * ip + 64);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const vkf_u4 v = *(const vkf_u4a4 *)(p + 128 + 32 * ip + 16 * k);
+        r.qh[4 * k] = v[0]; r.qh[4 * k + 1] = v[1]; r.qh[4 * k + 2] = v[2]; r.qh[4 * k + 3] = v[3];
+    }
+    r.qh[8] = *(const uint32_t *)(p + 128 + 32 * ip + 32);
+    r.sc[0] = *(const uint32_t *)(p + 192 + 8 * ip);
+    r.sc[1] = *(const uint32_t *)(p + 196 + 8 * ip);
+    r.sc[2] = *(const uint32_t *)(p + ((sb & 1) ? 200 + 8 * ip : 196 + 8 * ip));
+    r.d = *(const uint16_t *)(row + 210u * sb + 208);
+}
+
+// sum over the chunk for activation row m: d_w * sum_t dx(t) * Q_t
+template <int MM>
+__device__ __forceinline__ float q6_chunk(const Q6Raw &r, uint32_t sh, const unsigned char *lds, uint32_t m,
+                                          uint32_t c) {
+    // realigned fields (sh = 0 or 2 bytes); ql words are realigned where they
+    // are used (each serves two blocks), qh once
+    uint32_t qh[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) qh[i] = __builtin_amdgcn_alignbyte(r.qh[i + 1], r.qh[i], sh);
+    const uint32_t s0 = __builtin_amdgcn_alignbyte(r.sc[1], r.sc[0], sh);
+    const uint32_t s1 = __builtin_amdgcn_alignbyte(r.sc[2], r.sc[1], sh);
+    const float dw = vkf_h2f(r.d);
+    const vkf_f4 dx = *(const vkf_f4 *)q6_plane<MM>((unsigned char *)lds, m, 8, c);
+    const vkf_i4 X0 = *(const vkf_i4 *)q6_plane<MM>((unsigned char *)lds, m, 9, c);
+    const vkf_i4 X1 = *(const vkf_i4 *)q6_plane<MM>((unsigned char *)lds, m, 10, c);
+    float acc = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const vkf_u4 xa = *(const vkf_u4 *)q6_plane<MM>((unsigned char *)lds, m, 2 * t, c);
+        const vkf_u4 xb = *(const vkf_u4 *)q6_plane<MM>((unsigned char *)lds, m, 2 * t + 1, c);
+        int p0 = 0, p1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            // element 4i..4i+3 of block t: low nibble (t < 2) or high nibble
+            // of ql[32(t&1) + 4i ..], bits 2t, 2t+1 of qh[4i ..]
+            const int w = 8 * (t & 1) + i;
+            const uint32_t l = __builtin_amdgcn_alignbyte(r.ql[w + 1], r.ql[w], sh);
+            const uint32_t lo = (t >> 1) ? ((l >> 4) & 0x0f0f0f0fu) : (l & 0x0f0f0f0fu);
+            const uint32_t hs = t == 0 ? (qh[i] << 4) : t == 1 ? (qh[i] << 2) : t == 2 ? qh[i] : (qh[i] >> 2);
+            const uint32_t u = (hs & 0x30303030u) | lo;
+            if (i < 4) p0 = __builtin_amdgcn_sdot4((int)u, (int)xa[i], p0, false);
+            else p1 = __builtin_amdgcn_sdot4((int)u, (int)xb[i - 4], p1, false);
+        }
+        // int8 scales of the two 16-element halves: bytes 2t, 2t+1
+        const uint32_t sw = t < 2 ? s0 : s1;
+        const int sc0 = (int)(int8_t)(sw >> (16 * (t & 1))), sc1 = (int)(int8_t)(sw >> (16 * (t & 1) + 8));
+        const int Q = sc0 * (p0 - 32 * X0[t]) + sc1 * (p1 - 32 * X1[t]);
+        acc = fmaf(dx[t], (float)Q, acc);
+    }
+    return dw * acc;
+}
+
+// flags bit 0: y += instead of y =; bits 8..15: S (lanes per row segment,
+// a power of two 8..64).  Dynamic LDS: MM * 11 * q6_plane_bytes<MM>().
+template <int MM>
+__device__ __forceinline__ void gemv_q6k_q81(const VkfGemvArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const uint32_t C = a.K / 128, M = a.M, nkb = a.K / 32;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t S = (a.flags >> 8) & 0xffu;
+    const uint32_t seg = lane / S, p = lane & (S - 1);
+    const uint32_t TR = 64 / S;  // rows per wave tile
+    const uint32_t ntiles = (a.N + TR - 1) / TR;
+    const uint32_t iters = (C + S - 1) / S;
+    const uint32_t tstep = gridDim.x * Q6_WAVES;
+
+    for (uint32_t i = threadIdx.x; i < M * nkb; i += blockDim.x) {
+        const uint32_t m = i / nkb;
+        q6_stage_block<MM>(a, smem, m, i - m * nkb);
+    }
+    __syncthreads();
+
+    for (uint32_t tile = wave * gridDim.x + blockIdx.x; tile < ntiles; tile += tstep) {
+        const uint32_t n = tile * TR + seg;
+        const uint8_t *row = a.w + (uint64_t)(n < a.N ? n : 0) * a.row_bytes;
+        float acc[MM];
+#pragma unroll
+        for (int m = 0; m < MM; m++) acc[m] = 0.0f;
+        // one chunk in flight per lane; the 16 waves of a CU overlap each
+        // other's loads
+        for (uint32_t it = 0; it < iters; it++) {
+            const uint32_t c = p + it * S;
+            if (c < C) {
+                Q6Raw r;
+                q6_load(row, c, r);
+                const uint32_t sh = 2u * ((c >> 1) & 1u);
+#pragma unroll
+                for (int m = 0; m < MM; m++)
+                    if (MM == 1 || m < (int)M) acc[m] += q6_chunk<MM>(r, sh, smem, m, c);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MM; m++) {
+            float v = acc[m];
+            for (uint32_t o = S >> 1; o > 0; o >>= 1) v += __shfl_xor(v, (int)o, 64);
+            if (p == 0 && m < (int)M && n < a.N) {
+                float *yp = a.y + (uint64_t)m * a.ldy + n;
+                *yp = (a.flags & 1u) ? *yp + v : v;
+            }
+        }
+    }
+}
+
+VKF_KERNEL void __launch_bounds__(64 * Q6_WAVES) vkf_gemv_q6k_q81_dot_m1(VkfGemvArgs a) { gemv_q6k_q81<1>(a); }
