@@ -252,6 +252,101 @@ __device__ __forceinline__ void gemm_mainloop(const OX &ox, const OY &oy, uint32
     }
 }
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS pipeline for dense operands that are K-contiguous, 16-byte
+// aligned rows, with K*ES a multiple of 128 (the common case; everything
+// else takes gemm_mainloop).  global_load_lds_dwordx4 writes each lane's 16
+// bytes straight into LDS (slot = lane), so no registers stage the tiles:
+// the next step loads while this one is multiplied.  Tile layout per stage and operand: 128
+// rows x 128 bytes, 16-byte chunk c of row r at r*128 + ((c ^ (r & 7)) * 16)
+// (the XOR spreads the 16 rows of a fragment read over all banks); a load
+// instruction covers 8 rows x 8 chunks, lane L taking chunk (L%8) ^ (row&7)
+// of row L/8 so that its slot lands on that position.
+// ---------------------------------------------------------------------------
+#define GNST 2
+// two stages (64 KiB) or the epilogue's fp32 tile (128 x 132 floats), the
+// larger; two workgroups fit a CU (measured faster than three or four stages
+// with one workgroup per CU)
+#define GEMM_LDS_DMA (GNST * 32768 > 128 * 132 * 4 ? GNST * 32768 : 128 * 132 * 4)
+#define GEMM_LDS_BOTH (GEMM_LDS_DMA > GEMM_LDS ? GEMM_LDS_DMA : GEMM_LDS)
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else static_assert(N == 0, "wait_vm: unsupported count");
+}
+
+__device__ __forceinline__ bool dma_ok(const void *P, uint64_t ld, bool trans, uint32_t K, int ES) {
+    return !trans && ((ld * ES) % 16) == 0 && (((uintptr_t)P & 15) == 0) && ((uint64_t)K * ES) % 128 == 0;
+}
+
+template <int ES, class ACC>
+__device__ __forceinline__ void gemm_mainloop_dma(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, ACC acc[4][4],
+                                                  uint8_t *smem) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wr = wave >> 1, wc = wave & 1;
+    const int li = lane & 15, lg = lane >> 4;
+    const uint32_t nk = (uint32_t)(((uint64_t)a.K * ES) / 128);
+    const uint8_t *gx[4], *gy[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t rr = (4 * wave + j) * 8 + (lane >> 3);
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t rx = r0 + rr < a.R ? r0 + rr : a.R - 1;  // rows past the edge: any valid row
+        const uint32_t ry = c0 + rr < a.Cn ? c0 + rr : a.Cn - 1;
+        gx[j] = (const uint8_t *)a.X + (uint64_t)rx * a.ldx * ES + ch * 16;
+        gy[j] = (const uint8_t *)a.Y + (uint64_t)ry * a.ldy * ES + ch * 16;
+    }
+    auto issue = [&](uint32_t kt, uint32_t stage) {
+        uint8_t *sx = smem + stage * 32768, *sy = sx + 16384;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t off = (4 * wave + j) * 8 * 128;
+            __builtin_amdgcn_global_load_lds(gx[j] + (uint64_t)kt * 128, (__attribute__((address_space(3))) void *)(sx + off), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(gy[j] + (uint64_t)kt * 128, (__attribute__((address_space(3))) void *)(sy + off), 16, 0, 0);
+        }
+    };
+#pragma unroll
+    for (uint32_t s = 0; s + 1 < GNST; s++)
+        if (s < nk) issue(s, s);
+    const int sw = li & 7;
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        // this thread's loads of step kt are done when at most the loads of
+        // the (up to GNST-2) later steps are outstanding
+        if (kt + GNST - 2 < nk) wait_vm<8 * (GNST - 2)>();
+        else wait_vm<0>();
+        __syncthreads();
+        if (kt + GNST - 1 < nk) issue(kt + GNST - 1, (kt + GNST - 1) % GNST);
+        const uint8_t *lx = smem + (kt % GNST) * 32768, *ly = lx + 16384;
+        vkf_i4 fa[2][4], fb[2][4];
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int c = 4 * s + lg;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                fa[s][i] = *(const vkf_i4 *)(lx + (wr * 64 + 16 * i + li) * 128 + ((c ^ sw) << 4));
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                fb[s][j] = *(const vkf_i4 *)(ly + (wc * 64 + 16 * j + li) * 128 + ((c ^ sw) << 4));
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    if constexpr (ES == 2)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vkf_h8, fa[s][i]),
+                                                                           __builtin_bit_cast(vkf_h8, fb[s][j]),
+                                                                           acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
+                }
+    }
+    __syncthreads();  // LDS free for the epilogue
+}
+
 // Float epilogue (epi_store's arithmetic) of the workgroup's 128x128 tile:
 // each lane finishes its 64 values, the tile is staged as fp32 rows in LDS
 // (pitch 132 floats) and written out as 16-byte row vectors when D's rows
@@ -353,7 +448,16 @@ __device__ __forceinline__ void gemm_f16_body(const VkfGemmArgs &a) {
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
-    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_LDS];
+    // dense x dense kernels hold either main loop's buffers
+    __shared__ __attribute__((aligned(16))) uint8_t smem[(XQT < 0 && QT < 0) ? GEMM_LDS_BOTH : GEMM_LDS];
+    if constexpr (XQT < 0 && QT < 0) {
+        if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 2) &&
+            dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 2)) {
+            gemm_mainloop_dma<2>(a, r0, c0, acc, smem);
+            epilogue_tile(a, r0, c0, acc, smem);
+            return;
+        }
+    }
     const auto ox = make_operand<2, XQT>(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.R, r0, a.K);
     const auto oy = make_operand<2, QT>(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.Cn, c0, a.K);
     gemm_mainloop<2>(ox, oy, a.K, 64, acc, smem);
@@ -387,16 +491,21 @@ VKF_GEMM_Q_Q81(q5_k, VKF_Q5_K)
 // stores the raw int32 accumulator.
 // ---------------------------------------------------------------------------
 GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_LDS];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_LDS_BOTH];
     const uint32_t r0 = blockIdx.y * 128, c0 = blockIdx.x * 128;
     vkf_i4 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = vkf_i4{0, 0, 0, 0};
-    const auto ox = make_operand<1, -1>(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.R, r0, a.K);
-    const auto oy = make_operand<1, -1>(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.Cn, c0, a.K);
-    gemm_mainloop<1>(ox, oy, a.K, 128, acc, smem);
+    if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 1) &&
+        dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 1)) {
+        gemm_mainloop_dma<1>(a, r0, c0, acc, smem);
+    } else {
+        const auto ox = make_operand<1, -1>(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.R, r0, a.K);
+        const auto oy = make_operand<1, -1>(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.Cn, c0, a.K);
+        gemm_mainloop<1>(ox, oy, a.K, 128, acc, smem);
+    }
     if (!(a.flags & VKF_GF_D_I32)) {
         epilogue_tile(a, r0, c0, acc, smem);
         return;
