@@ -347,6 +347,144 @@ __device__ __forceinline__ void gemm_mainloop_dma(const VkfGemmArgs &a, uint32_t
     __syncthreads();  // LDS free for the epilogue
 }
 
+// ---------------------------------------------------------------------------
+// Quantised-weight GEMM with dense fp16 activations: X by direct-to-LDS
+// loads, the weight tile staged through registers.  Each 64-k step, thread
+// t owns weight row t/2 and its 32-element chunk (t&1): QStage<QT>::load
+// issues the chunk's global loads (before the MFMAs of the current step),
+// ::decode turns them into the reference's exact fp32 values rounded to
+// fp16 (after the MFMAs, so the load latency hides under them), and the
+// tile is written to LDS in the same XOR-swizzled layout as X.
+// ---------------------------------------------------------------------------
+template <int QT>
+struct QStage {  // any format: decode8 on the spot (load waits for its data)
+    TileRegs t;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        load_quant<QT>(W, row_bytes, nrows, row0, K, k0, t);
+    }
+    __device__ __forceinline__ void decode(TileRegs &out) { out = t; }
+};
+
+// Q4_K: one 32-element chunk = sub-block j of a super-block: header (dall,
+// dmin, 6-bit scales) + the 32 qs bytes of the sub-block pair, nibble j&1
+// (kernels/dequant_q4_k.glsl:16-24, 49-57).  Value = fma(dall*sc, q, -dmin*m)
+// in fp32 (dall*sc and its product with q are exact, so this is the
+// reference's single rounding), then fp16 round-to-nearest-even.
+template <>
+struct QStage<VKF_Q4_K> {
+    vkf_u4 hdr, qa, qb;
+    uint32_t j;
+    bool live;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        const uint32_t r = row0 + (threadIdx.x >> 1), kc = k0 + 32 * (threadIdx.x & 1);
+        live = r < nrows && kc < K;
+        const uint32_t rr = r < nrows ? r : nrows - 1, kk = kc < K ? kc : 0;
+        const uint8_t *blk = W + (uint64_t)rr * row_bytes + 144ull * (kk / 256);
+        j = (kk % 256) / 32;
+        hdr = *(const vkf_u4 *)blk;
+        const uint8_t *q = blk + 16 + 32 * (j >> 1);
+        qa = *(const vkf_u4 *)q;
+        qb = *(const vkf_u4 *)(q + 16);
+    }
+    __device__ __forceinline__ void decode(TileRegs &out) {
+        const float dall = vkf_h2f(hdr[0] & 0xffffu), dmin = vkf_h2f(hdr[0] >> 16);
+        const uint32_t s0 = hdr[1], s4 = hdr[2], s8 = hdr[3];
+        const uint32_t scW = j < 4 ? (s0 & 0x3f3f3f3fu) : ((s8 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u));
+        const uint32_t mnW = j < 4 ? (s4 & 0x3f3f3f3fu) : (((s8 >> 4) & 0x0f0f0f0fu) | ((s4 >> 2) & 0x30303030u));
+        const uint32_t sh = 8 * (j & 3);
+        const float dsc = dall * (float)((scW >> sh) & 0xffu), dm = dmin * (float)((mnW >> sh) & 0xffu);
+        const uint32_t nsh = 4 * (j & 1);
+        uint32_t w[8] = {qa[0], qa[1], qa[2], qa[3], qb[0], qb[1], qb[2], qb[3]};
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            vkf_h8 h;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t n = (w[2 * g + e] >> nsh) & 0x0f0f0f0fu;
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    h[4 * e + k] = vkf_to_f16(fmaf(dsc, (float)((n >> (8 * k)) & 0xffu), -dm));
+            }
+            out.v[g] = live ? __builtin_bit_cast(vkf_i4, h) : vkf_i4{0, 0, 0, 0};
+        }
+    }
+};
+
+template <int QT>
+__device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, vkf_f4 acc[4][4],
+                                                   uint8_t *smem) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wr = wave >> 1, wc = wave & 1;
+    const int li = lane & 15, lg = lane >> 4;
+    const uint32_t nk = a.K / 64;
+    const uint8_t *gx[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t rr = (4 * wave + j) * 8 + (lane >> 3);
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t rx = r0 + rr < a.R ? r0 + rr : a.R - 1;
+        gx[j] = (const uint8_t *)a.X + (uint64_t)rx * a.ldx * 2 + ch * 16;
+    }
+    auto issue_x = [&](uint32_t kt, uint32_t stage) {
+        uint8_t *sx = smem + stage * 32768;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            __builtin_amdgcn_global_load_lds(gx[j] + (uint64_t)kt * 128,
+                                             (__attribute__((address_space(3))) void *)(sx + (4 * wave + j) * 1024),
+                                             16, 0, 0);
+    };
+    const uint32_t yr = threadIdx.x >> 1, yh = threadIdx.x & 1;
+    auto store_y = [&](uint32_t stage, const TileRegs &t) {
+        uint8_t *sy = smem + stage * 32768 + 16384 + yr * 128;
+#pragma unroll
+        for (int g = 0; g < 4; g++) *(vkf_i4 *)(sy + (((4 * yh + g) ^ (yr & 7)) << 4)) = t.v[g];
+    };
+    QStage<QT> q;
+    TileRegs ty;
+    issue_x(0, 0);
+    q.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, 0);
+    q.decode(ty);
+    store_y(0, ty);
+    wait_vm<0>();
+    __syncthreads();
+    const int sw = li & 7;
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        const uint32_t cur = kt & 1;
+        if (kt + 1 < nk) {
+            issue_x(kt + 1, cur ^ 1);
+            q.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, (kt + 1) * 64);
+        }
+        const uint8_t *lx = smem + cur * 32768, *ly = lx + 16384;
+        vkf_i4 fa[2][4], fb[2][4];
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int c = 4 * s + lg;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                fa[s][i] = *(const vkf_i4 *)(lx + (wr * 64 + 16 * i + li) * 128 + ((c ^ sw) << 4));
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                fb[s][j] = *(const vkf_i4 *)(ly + (wc * 64 + 16 * j + li) * 128 + ((c ^ sw) << 4));
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vkf_h8, fa[s][i]),
+                                                                       __builtin_bit_cast(vkf_h8, fb[s][j]),
+                                                                       acc[i][j], 0, 0, 0);
+        if (kt + 1 < nk) {
+            q.decode(ty);
+            store_y(cur ^ 1, ty);
+        }
+        wait_vm<0>();
+        __syncthreads();
+    }
+}
+
 // Float epilogue (epi_store's arithmetic) of the workgroup's 128x128 tile:
 // each lane finishes its 64 values, the tile is staged as fp32 rows in LDS
 // (pitch 132 floats) and written out as 16-byte row vectors when D's rows
@@ -448,12 +586,19 @@ __device__ __forceinline__ void gemm_f16_body(const VkfGemmArgs &a) {
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
-    // dense x dense kernels hold either main loop's buffers
-    __shared__ __attribute__((aligned(16))) uint8_t smem[(XQT < 0 && QT < 0) ? GEMM_LDS_BOTH : GEMM_LDS];
+    // kernels with dense fp16 X hold either main loop's buffers
+    __shared__ __attribute__((aligned(16))) uint8_t smem[XQT < 0 ? GEMM_LDS_BOTH : GEMM_LDS];
     if constexpr (XQT < 0 && QT < 0) {
         if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 2) &&
             dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 2)) {
             gemm_mainloop_dma<2>(a, r0, c0, acc, smem);
+            epilogue_tile(a, r0, c0, acc, smem);
+            return;
+        }
+    }
+    if constexpr (XQT < 0 && QT >= 0) {
+        if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 2)) {
+            gemm_mainloop_qdma<QT>(a, r0, c0, acc, smem);
             epilogue_tile(a, r0, c0, acc, smem);
             return;
         }

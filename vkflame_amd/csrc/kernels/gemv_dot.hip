@@ -36,8 +36,6 @@
 #define DOT_WAVES 16
 #define DOT_PLANE 4096  // bytes per LDS plane: chunks c < 256, K <= 16384
 
-typedef unsigned int vkf_u4 __attribute__((ext_vector_type(4)));
-typedef unsigned int vkf_u2 __attribute__((ext_vector_type(2)));
 // Vectors at 4- / 8-byte aligned addresses (Q4_0 / Q8_0 block pairs start on
 // 4-byte boundaries, Q4_1 pairs on 8): still one global_load_dwordx4 each.
 typedef unsigned int vkf_u4a4 __attribute__((ext_vector_type(4), aligned(4)));

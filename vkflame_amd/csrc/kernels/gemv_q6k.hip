@@ -29,7 +29,6 @@
 // MM = 4 up to 128 (K <= 16384)
 template <int MM> constexpr uint32_t q6_plane_bytes() { return MM == 1 ? 4096 : 2048; }
 
-typedef unsigned int vkf_u4 __attribute__((ext_vector_type(4)));
 typedef unsigned int vkf_u4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 // LDS image of MM activation rows, per chunk c (4 Q8_1 blocks t = 0..3):

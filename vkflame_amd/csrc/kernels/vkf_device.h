@@ -15,6 +15,8 @@ typedef float vkf_f4 __attribute__((ext_vector_type(4)));
 typedef float vkf_f16v __attribute__((ext_vector_type(16)));
 typedef int vkf_i4 __attribute__((ext_vector_type(4)));
 typedef int vkf_i2 __attribute__((ext_vector_type(2)));
+typedef unsigned int vkf_u4 __attribute__((ext_vector_type(4)));
+typedef unsigned int vkf_u2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float vkf_h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
