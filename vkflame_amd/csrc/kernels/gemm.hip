@@ -63,6 +63,8 @@ __device__ __forceinline__ void epi_store(const VkfGemmArgs &a, uint32_t r, uint
 // MFMAs per wave between barriers.
 // ---------------------------------------------------------------------------
 #define GK 128  // bytes of K per step and operand row
+
+typedef unsigned int vkf_u4a4 __attribute__((ext_vector_type(4), aligned(4)));
 #define GP 160  // LDS row pitch (bytes)
 
 struct TileRegs {
@@ -406,6 +408,115 @@ struct QStage<VKF_Q4_K> {
 #pragma unroll
                 for (int k = 0; k < 4; k++)
                     h[4 * e + k] = vkf_to_f16(fmaf(dsc, (float)((n >> (8 * k)) & 0xffu), -dm));
+            }
+            out.v[g] = live ? __builtin_bit_cast(vkf_i4, h) : vkf_i4{0, 0, 0, 0};
+        }
+    }
+};
+
+// 32-element blocks at 2-byte aligned addresses (Q4_0 18 B, Q8_0 34 B): the
+// block's bytes are loaded as the 4-byte aligned dwords that cover them and
+// realigned by sh = block address & 3 (0 or 2); no load reaches past the
+// block's last byte.
+__device__ __forceinline__ uint32_t realign(uint32_t lo, uint32_t hi, uint32_t sh) {
+    return __builtin_amdgcn_alignbyte(hi, lo, sh);
+}
+
+// Q4_0: value d*q + (-8d) (kernels/dequant_q4_0.glsl:30-35; d*q exact).
+template <>
+struct QStage<VKF_Q4_0> {
+    uint32_t r[5], sh;
+    bool live;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        const uint32_t rw = row0 + (threadIdx.x >> 1), kc = k0 + 32 * (threadIdx.x & 1);
+        live = rw < nrows && kc < K;
+        const uint8_t *blk = W + (uint64_t)(rw < nrows ? rw : nrows - 1) * row_bytes + 18ull * ((kc < K ? kc : 0) / 32);
+        sh = (uint32_t)(uintptr_t)blk & 3u;
+        const uint8_t *a = blk - sh;
+        const vkf_u4 v = *(const vkf_u4a4 *)a;
+        r[0] = v[0]; r[1] = v[1]; r[2] = v[2]; r[3] = v[3];
+        r[4] = sh ? *(const uint32_t *)(a + 16) : (uint32_t)*(const uint16_t *)(blk + 16);
+    }
+    __device__ __forceinline__ void decode(TileRegs &out) {
+        // d at bytes sh..sh+1, qs at sh+2 .. sh+17
+        const float d = vkf_h2f((uint16_t)(realign(r[0], r[1], sh) & 0xffffu)), dm = -8.0f * d;
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[i] = sh ? r[i + 1] : realign(r[i], r[i + 1], 2);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {  // elements 8g .. 8g+7
+            vkf_h8 h;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int el = 8 * g + e, byte = el & 15;
+                const uint32_t nib = (q[byte >> 2] >> (8 * (byte & 3) + 4 * (el >> 4))) & 0xfu;
+                h[e] = vkf_to_f16(fmaf(d, (float)nib, dm));
+            }
+            out.v[g] = live ? __builtin_bit_cast(vkf_i4, h) : vkf_i4{0, 0, 0, 0};
+        }
+    }
+};
+
+// Q4_1: value d*q + m (kernels/dequant_q4_1.glsl; 20-byte blocks are 4-byte
+// aligned).
+template <>
+struct QStage<VKF_Q4_1> {
+    uint32_t r[5];
+    bool live;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        const uint32_t rw = row0 + (threadIdx.x >> 1), kc = k0 + 32 * (threadIdx.x & 1);
+        live = rw < nrows && kc < K;
+        const uint8_t *blk = W + (uint64_t)(rw < nrows ? rw : nrows - 1) * row_bytes + 20ull * ((kc < K ? kc : 0) / 32);
+        const vkf_u4 v = *(const vkf_u4a4 *)blk;
+        r[0] = v[0]; r[1] = v[1]; r[2] = v[2]; r[3] = v[3];
+        r[4] = *(const uint32_t *)(blk + 16);
+    }
+    __device__ __forceinline__ void decode(TileRegs &out) {
+        const float d = vkf_h2f((uint16_t)(r[0] & 0xffffu)), m = vkf_h2f((uint16_t)(r[0] >> 16));
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            vkf_h8 h;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int el = 8 * g + e, byte = el & 15;
+                const uint32_t nib = (r[1 + (byte >> 2)] >> (8 * (byte & 3) + 4 * (el >> 4))) & 0xfu;
+                h[e] = vkf_to_f16(fmaf(d, (float)nib, m));
+            }
+            out.v[g] = live ? __builtin_bit_cast(vkf_i4, h) : vkf_i4{0, 0, 0, 0};
+        }
+    }
+};
+
+// Q8_0: value d*q (exact), 34-byte blocks.
+template <>
+struct QStage<VKF_Q8_0> {
+    uint32_t r[9], sh;
+    bool live;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        const uint32_t rw = row0 + (threadIdx.x >> 1), kc = k0 + 32 * (threadIdx.x & 1);
+        live = rw < nrows && kc < K;
+        const uint8_t *blk = W + (uint64_t)(rw < nrows ? rw : nrows - 1) * row_bytes + 34ull * ((kc < K ? kc : 0) / 32);
+        sh = (uint32_t)(uintptr_t)blk & 3u;
+        const uint8_t *a = blk - sh;
+        const vkf_u4 v0 = *(const vkf_u4a4 *)a, v1 = *(const vkf_u4a4 *)(a + 16);
+        r[0] = v0[0]; r[1] = v0[1]; r[2] = v0[2]; r[3] = v0[3];
+        r[4] = v1[0]; r[5] = v1[1]; r[6] = v1[2]; r[7] = v1[3];
+        r[8] = sh ? *(const uint32_t *)(a + 32) : (uint32_t)*(const uint16_t *)(blk + 32);
+    }
+    __device__ __forceinline__ void decode(TileRegs &out) {
+        const float d = vkf_h2f((uint16_t)(realign(r[0], r[1], sh) & 0xffffu));
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            vkf_h8 h;
+#pragma unroll
+            for (int e2 = 0; e2 < 2; e2++) {
+                const int i = 2 * g + e2;  // qs dword i = bytes sh+2+4i ..
+                const uint32_t q = sh ? r[i + 1] : realign(r[i], r[i + 1], 2);
+#pragma unroll
+                for (int k = 0; k < 4; k++) h[4 * e2 + k] = vkf_to_f16(d * (float)(int8_t)(q >> (8 * k)));
             }
             out.v[g] = live ? __builtin_bit_cast(vkf_i4, h) : vkf_i4{0, 0, 0, 0};
         }
