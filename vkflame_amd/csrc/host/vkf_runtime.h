@@ -87,7 +87,7 @@
     X(GEMM_Q5_K_F16, "vkf_gemm_q5_k_f16")                   \
     X(GEMM_Q5_K_Q81, "vkf_gemm_q5_k_q8_1")                  \
     X(GEMM_Q6_K_F16, "vkf_gemm_q6_k_f16")                   \
-    X(GEMM_Q6_K_Q81, "vkf_gemm_q6_k_q8_1_int")
+    X(GEMM_Q6_K_Q81, "vkf_gemm_q6_k_q8_1")
 
 enum VkfKernelId {
 #define VKF_X(id, sym) VKF_K_##id,

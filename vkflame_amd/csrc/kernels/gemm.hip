@@ -6,51 +6,32 @@
 //
 // Core: D[r, c] = epi( sum_k X[r, k] * Y[c, k] ) with both operands
 // K-contiguous.  A 256-thread workgroup owns a 128x128 tile of D; each of its
-// four waves owns 64x64 = 4x4 MFMA 16x16 sub-tiles.  K advances in steps that
-// are staged through double-buffered LDS, one barrier per step.
-//
-// Variants (all share the tiling):
+// four waves owns 64x64 = 4x4 MFMA 16x16 sub-tiles.  K advances 128 bytes of
+// each operand row per step through two LDS buffers, one barrier per step.
+// Main loops (chosen per call, all sharing the tiling and the epilogue):
+//   gemm_mainloop_dma   dense, aligned operands: global_load_lds straight
+//                       into XOR-swizzled LDS tiles (fp16 and int8)
+//   gemm_mainloop_qdma  dense fp16 activations by direct-to-LDS loads x ggml
+//                       weight tiles loaded before and decoded after each
+//                       step's MFMAs (QStage<format>)
+//   gemm_mainloop_qq    Q8_1 activations x ggml weights, both decoded that way
+//   gemm_mainloop       anything else (transposed, ragged K, unaligned):
+//                       register-staged tiles, padded LDS rows
+// Kernels:
 //   vkf_gemm_f16        fp16 x fp16 -> fp32 acc, v_mfma_f32_16x16x32_f16
-//   vkf_gemm_i8         int8 x int8 -> int32 acc, v_mfma_i32_16x16x64_i8
-//   vkf_gemm_<q>_f16    fp16 activations x ggml weights: each weight tile is
-//                       dequantised in registers to the reference's exact fp32
-//                       value, rounded to fp16 and written to LDS, then the
-//                       fp16 MFMA core runs (dequant fused into the GEMM)
-//   vkf_gemm_q6_k_q8_1  Q8_1 activations x Q6_K weights, integer-exact: LDS
-//                       holds q8 and sc*(q6-32) as fp16 (both exact integers),
-//                       so each 32-deep MFMA yields the exact integer partial
-//                       P[m,n,kb]; the fp32 epilogue applies dx per block and
-//                       dw per super-block.
+//   vkf_gemm_i8         int8 x int8 -> int32 acc (exact), v_mfma_i32_16x16x64_i8
+//   vkf_gemm_<q>_f16    fp16 activations x ggml weights dequantised to the
+//                       reference's exact fp32 value, rounded to fp16
+//   vkf_gemm_<q>_q8_1   Q8_1 activations as fp16(d*q) x ggml weights as above
+//                       (fp32 accumulation; the products of two fp16-rounded
+//                       operands are within the float tolerance, not integer
+//                       exact)
 //
 // MFMA 16x16 operand layout used throughout: lane l supplies row (l % 16) of
 // A and column (l % 16) of B, with a K slice selected by l / 16; both operands
 // use the same K slice map, so the product is independent of the hardware's
 // internal K order.  Accumulator: lane l holds D[4*(l/16) + i][l % 16].
 #include "vkf_device.h"
-
-#define BM 128
-#define BN 128
-#define PF 40  // fp16 LDS pitch of the Q6_K x Q8_1 kernel (32 k + 8 pad)
-
-__device__ __forceinline__ void epi_store(const VkfGemmArgs &a, uint32_t r, uint32_t c, float v) {
-    if (a.rs) v *= a.rs[(a.flags & VKF_GF_RS_SCALAR) ? 0 : r];
-    if (a.cs) v *= a.cs[(a.flags & VKF_GF_CS_SCALAR) ? 0 : c];
-    v *= a.alpha;
-    if (a.beta != 0.0f) {
-        float cin = (a.flags & VKF_GF_CIN_F32) ? ((const float *)a.Cin)[(uint64_t)r * a.ldc + c]
-                                                : (float)((const _Float16 *)a.Cin)[(uint64_t)r * a.ldc + c];
-        v = fmaf(a.beta, cin, v);
-    }
-    if (a.bias) {
-        uint32_t bi = (a.flags & VKF_GF_BIAS_ROW) ? r : c;
-        v += (a.flags & VKF_GF_BIAS_F32) ? ((const float *)a.bias)[bi] : (float)((const _Float16 *)a.bias)[bi];
-    }
-    v = vkf_act(a.act, v);
-    if (a.flags & VKF_GF_D_F32)
-        ((float *)a.D)[(uint64_t)r * a.ldd + c] = v;
-    else
-        ((_Float16 *)a.D)[(uint64_t)r * a.ldd + c] = vkf_to_f16(v);
-}
 
 // ---------------------------------------------------------------------------
 // Pipelined core shared by the fp16, int8 and quantised-weight kernels.
@@ -284,6 +265,36 @@ __device__ __forceinline__ bool dma_ok(const void *P, uint64_t ld, bool trans, u
     return !trans && ((ld * ES) % 16) == 0 && (((uintptr_t)P & 15) == 0) && ((uint64_t)K * ES) % 128 == 0;
 }
 
+// One step (128 bytes of K) of the wave's 64x64 tile from swizzled LDS tiles.
+template <int ES, class ACC>
+__device__ __forceinline__ void mfma_step_swz(const uint8_t *lx, const uint8_t *ly, int wr, int wc, ACC acc[4][4]) {
+    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4, sw = li & 7;
+    vkf_i4 fa[2][4], fb[2][4];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int c = 4 * s + lg;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            fa[s][i] = *(const vkf_i4 *)(lx + (wr * 64 + 16 * i + li) * 128 + ((c ^ sw) << 4));
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            fb[s][j] = *(const vkf_i4 *)(ly + (wc * 64 + 16 * j + li) * 128 + ((c ^ sw) << 4));
+    }
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if constexpr (ES == 2)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vkf_h8, fa[s][i]),
+                                                                       __builtin_bit_cast(vkf_h8, fb[s][j]),
+                                                                       acc[i][j], 0, 0, 0);
+                else
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
+            }
+}
+
 template <int ES, class ACC>
 __device__ __forceinline__ void gemm_mainloop_dma(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, ACC acc[4][4],
                                                   uint8_t *smem) {
@@ -320,31 +331,8 @@ __device__ __forceinline__ void gemm_mainloop_dma(const VkfGemmArgs &a, uint32_t
         else wait_vm<0>();
         __syncthreads();
         if (kt + GNST - 1 < nk) issue(kt + GNST - 1, (kt + GNST - 1) % GNST);
-        const uint8_t *lx = smem + (kt % GNST) * 32768, *ly = lx + 16384;
-        vkf_i4 fa[2][4], fb[2][4];
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const int c = 4 * s + lg;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                fa[s][i] = *(const vkf_i4 *)(lx + (wr * 64 + 16 * i + li) * 128 + ((c ^ sw) << 4));
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                fb[s][j] = *(const vkf_i4 *)(ly + (wc * 64 + 16 * j + li) * 128 + ((c ^ sw) << 4));
-        }
-#pragma unroll
-        for (int s = 0; s < 2; s++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    if constexpr (ES == 2)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vkf_h8, fa[s][i]),
-                                                                           __builtin_bit_cast(vkf_h8, fb[s][j]),
-                                                                           acc[i][j], 0, 0, 0);
-                    else
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
-                }
+        const uint8_t *lx = smem + (kt % GNST) * 32768;
+        mfma_step_swz<ES>(lx, lx + 16384, wr, wc, acc);
     }
     __syncthreads();  // LDS free for the epilogue
 }
@@ -523,6 +511,134 @@ struct QStage<VKF_Q8_0> {
     }
 };
 
+// Q8_1 activation blocks (36 bytes, 4-byte aligned: fp16 d, fp16 s, int8
+// q[32]) as an fp16 operand: fp16(d*q), the RNE of the exact product.
+template <>
+struct QStage<VKF_Q8_1> {
+    uint32_t r[9];
+    bool live;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        const uint32_t rw = row0 + (threadIdx.x >> 1), kc = k0 + 32 * (threadIdx.x & 1);
+        live = rw < nrows && kc < K;
+        const uint8_t *blk = W + (uint64_t)(rw < nrows ? rw : nrows - 1) * row_bytes + 36ull * ((kc < K ? kc : 0) / 32);
+        const vkf_u4 v0 = *(const vkf_u4a4 *)blk, v1 = *(const vkf_u4a4 *)(blk + 16);
+        r[0] = v0[0]; r[1] = v0[1]; r[2] = v0[2]; r[3] = v0[3];
+        r[4] = v1[0]; r[5] = v1[1]; r[6] = v1[2]; r[7] = v1[3];
+        r[8] = *(const uint32_t *)(blk + 32);
+    }
+    __device__ __forceinline__ void decode(TileRegs &out) {
+        const float d = vkf_h2f((uint16_t)(r[0] & 0xffffu));
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            vkf_h8 h;
+#pragma unroll
+            for (int e2 = 0; e2 < 2; e2++) {
+                const uint32_t q = r[1 + 2 * g + e2];
+#pragma unroll
+                for (int k = 0; k < 4; k++) h[4 * e2 + k] = vkf_to_f16(d * (float)(int8_t)(q >> (8 * k)));
+            }
+            out.v[g] = live ? __builtin_bit_cast(vkf_i4, h) : vkf_i4{0, 0, 0, 0};
+        }
+    }
+};
+
+// Q6_K: 32-element block t of half ip of a 210-byte super-block
+// (kernels/dequant_q6_k.glsl:34-58): u = low or high nibble of
+// ql[64ip + 32(t&1) + l] | bits 2t, 2t+1 of qh[32ip + l] << 4, value
+// d * sc * (u - 32) with sc = scales[8ip + 2t + l/16] (exact in fp32; the
+// fma below forms it without rounding), then fp16.  Fields are 2-byte
+// aligned: loaded as covering dwords and realigned, scales and d as 2-byte
+// loads, nothing past the super-block.
+template <>
+struct QStage<VKF_Q6_K> {
+    uint32_t ql[9], qh[9], sc, dd, sh, t;
+    bool live;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        const uint32_t rw = row0 + (threadIdx.x >> 1), kc = k0 + 32 * (threadIdx.x & 1);
+        live = rw < nrows && kc < K;
+        const uint32_t kk = kc < K ? kc : 0, j8 = (kk % 256) / 32, ip = j8 >> 2;
+        t = j8 & 3;
+        const uint8_t *blk = W + (uint64_t)(rw < nrows ? rw : nrows - 1) * row_bytes + 210ull * (kk / 256);
+        sh = (uint32_t)(uintptr_t)blk & 3u;
+        const uint8_t *a = blk - sh;  // 4-byte aligned
+        const uint8_t *pl = a + 64 * ip + 32 * (t & 1), *ph = a + 128 + 32 * ip;
+        const vkf_u4 l0 = *(const vkf_u4a4 *)pl, l1 = *(const vkf_u4a4 *)(pl + 16);
+        const vkf_u4 h0 = *(const vkf_u4a4 *)ph, h1 = *(const vkf_u4a4 *)(ph + 16);
+        ql[0] = l0[0]; ql[1] = l0[1]; ql[2] = l0[2]; ql[3] = l0[3];
+        ql[4] = l1[0]; ql[5] = l1[1]; ql[6] = l1[2]; ql[7] = l1[3];
+        qh[0] = h0[0]; qh[1] = h0[1]; qh[2] = h0[2]; qh[3] = h0[3];
+        qh[4] = h1[0]; qh[5] = h1[1]; qh[6] = h1[2]; qh[7] = h1[3];
+        // the dword after each field: inside the super-block (ql ends at
+        // byte <= 132, qh at <= 196); only needed when sh = 2
+        ql[8] = *(const uint32_t *)(pl + 32);
+        qh[8] = *(const uint32_t *)(ph + 32);
+        sc = *(const uint16_t *)(blk + 192 + 8 * ip + 2 * t);
+        dd = *(const uint16_t *)(blk + 208);
+    }
+    __device__ __forceinline__ void decode(TileRegs &out) {
+        const float d = vkf_h2f((uint16_t)dd);
+        const float ds0 = d * (float)(int8_t)(sc & 0xffu), ds1 = d * (float)(int8_t)(sc >> 8);
+        const uint32_t nsh = 4 * (t >> 1), hsh = 2 * t;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const float ds = g < 2 ? ds0 : ds1, off = -32.0f * ds;
+            vkf_h8 h;
+#pragma unroll
+            for (int e2 = 0; e2 < 2; e2++) {
+                const int i = 2 * g + e2;
+                const uint32_t l = realign(ql[i], ql[i + 1], sh), hb = realign(qh[i], qh[i + 1], sh);
+                const uint32_t u = ((l >> nsh) & 0x0f0f0f0fu) | (((hb >> hsh) & 0x03030303u) << 4);
+#pragma unroll
+                for (int k = 0; k < 4; k++) h[4 * e2 + k] = vkf_to_f16(fmaf(ds, (float)((u >> (8 * k)) & 0xffu), off));
+            }
+            out.v[g] = live ? __builtin_bit_cast(vkf_i4, h) : vkf_i4{0, 0, 0, 0};
+        }
+    }
+};
+
+// Both operands quantised (Q8_1 activations x ggml weights): both tiles are
+// staged through registers with the same load-before / decode-after split.
+template <int XQT, int QT>
+__device__ __forceinline__ void gemm_mainloop_qq(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, vkf_f4 acc[4][4],
+                                                 uint8_t *smem) {
+    const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
+    const uint32_t nk = (a.K + 63) / 64;
+    const uint32_t tr = threadIdx.x >> 1, th = threadIdx.x & 1;
+    auto store = [&](uint8_t *tile, const TileRegs &t) {
+        uint8_t *p = tile + tr * 128;
+#pragma unroll
+        for (int g = 0; g < 4; g++) *(vkf_i4 *)(p + (((4 * th + g) ^ (tr & 7)) << 4)) = t.v[g];
+    };
+    QStage<XQT> qx;
+    QStage<QT> qy;
+    TileRegs tx, ty;
+    qx.load((const uint8_t *)a.X, a.ldx, a.R, r0, a.K, 0);
+    qy.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, 0);
+    qx.decode(tx);
+    qy.decode(ty);
+    store(smem, tx);
+    store(smem + 16384, ty);
+    __syncthreads();
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        const uint32_t cur = kt & 1;
+        if (kt + 1 < nk) {
+            qx.load((const uint8_t *)a.X, a.ldx, a.R, r0, a.K, (kt + 1) * 64);
+            qy.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, (kt + 1) * 64);
+        }
+        const uint8_t *lx = smem + cur * 32768;
+        mfma_step_swz<2>(lx, lx + 16384, wr, wc, acc);
+        if (kt + 1 < nk) {
+            qx.decode(tx);
+            qy.decode(ty);
+            store(smem + (cur ^ 1) * 32768, tx);
+            store(smem + (cur ^ 1) * 32768 + 16384, ty);
+        }
+        __syncthreads();
+    }
+}
+
 template <int QT>
 __device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, vkf_f4 acc[4][4],
                                                    uint8_t *smem) {
@@ -566,27 +682,8 @@ __device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_
             issue_x(kt + 1, cur ^ 1);
             q.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, (kt + 1) * 64);
         }
-        const uint8_t *lx = smem + cur * 32768, *ly = lx + 16384;
-        vkf_i4 fa[2][4], fb[2][4];
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const int c = 4 * s + lg;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                fa[s][i] = *(const vkf_i4 *)(lx + (wr * 64 + 16 * i + li) * 128 + ((c ^ sw) << 4));
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                fb[s][j] = *(const vkf_i4 *)(ly + (wc * 64 + 16 * j + li) * 128 + ((c ^ sw) << 4));
-        }
-#pragma unroll
-        for (int s = 0; s < 2; s++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vkf_h8, fa[s][i]),
-                                                                       __builtin_bit_cast(vkf_h8, fb[s][j]),
-                                                                       acc[i][j], 0, 0, 0);
+        const uint8_t *lx = smem + cur * 32768;
+        mfma_step_swz<2>(lx, lx + 16384, wr, wc, acc);
         if (kt + 1 < nk) {
             q.decode(ty);
             store_y(cur ^ 1, ty);
@@ -596,7 +693,8 @@ __device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_
     }
 }
 
-// Float epilogue (epi_store's arithmetic) of the workgroup's 128x128 tile:
+// Float epilogue of the workgroup's 128x128 tile (v = alpha * acc * rs[r] *
+// cs[c] + beta * Cin + bias, then the activation):
 // each lane finishes its 64 values, the tile is staged as fp32 rows in LDS
 // (pitch 132 floats) and written out as 16-byte row vectors when D's rows
 // allow it, element by element otherwise.  smem must be free (the main loop
@@ -672,21 +770,6 @@ __device__ __forceinline__ void epilogue_tile(const VkfGemmArgs &a, uint32_t r0,
     }
 }
 
-// Per-element epilogue (the Q6_K x Q8_1 kernel's LDS layout differs).
-__device__ __forceinline__ void store_acc_f32(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, int wr, int wc,
-                                              vkf_f4 acc[4][4]) {
-    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                uint32_t r = r0 + wr * 64 + 16 * i + 4 * lg + e, c = c0 + wc * 64 + 16 * j + li;
-                if (r < a.R && c < a.Cn) epi_store(a, r, c, acc[i][j][e]);
-            }
-}
-
 // XQT < 0: dense fp16 X, otherwise Q8_1 activation blocks (each tile value
 // fp16(dx*q)).  QT < 0: dense fp16 Y; otherwise Y holds ggml blocks of type QT.
 template <int XQT, int QT>
@@ -714,6 +797,11 @@ __device__ __forceinline__ void gemm_f16_body(const VkfGemmArgs &a) {
             return;
         }
     }
+    if constexpr (XQT >= 0 && QT >= 0) {  // K is a multiple of 32 here
+        gemm_mainloop_qq<XQT, QT>(a, r0, c0, acc, smem);
+        epilogue_tile(a, r0, c0, acc, smem);
+        return;
+    }
     const auto ox = make_operand<2, XQT>(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.R, r0, a.K);
     const auto oy = make_operand<2, QT>(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.Cn, c0, a.K);
     gemm_mainloop<2>(ox, oy, a.K, 64, acc, smem);
@@ -740,6 +828,7 @@ VKF_GEMM_Q_Q81(q8_0, VKF_Q8_0)
 VKF_GEMM_Q_Q81(q5_0, VKF_Q5_0)
 VKF_GEMM_Q_Q81(q4_k, VKF_Q4_K)
 VKF_GEMM_Q_Q81(q5_k, VKF_Q5_K)
+VKF_GEMM_Q_Q81(q6_k, VKF_Q6_K)
 
 // ---------------------------------------------------------------------------
 // int8 x int8 -> int32 (kernels/linear_int8.glsl:54-93, with int8 A).
@@ -786,121 +875,3 @@ GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a) {
             }
 }
 
-// ---------------------------------------------------------------------------
-// Q6_K weights x Q8_1 activations, M >= 17.
-// X: Q8_1 rows (ldx bytes per row), Y: Q6_K rows (ldy bytes per row).
-// Per 32-deep step kb: LDS X = q8 (fp16, exact), Y = sc*(q6-32) (fp16,
-// exact, |.| <= 4096); one MFMA chain from zero gives P exactly (|P| < 2^24);
-//   accs += dx[m, kb] * P;  at each 256 boundary: acc += dw[n, sb] * accs.
-// ---------------------------------------------------------------------------
-VKF_KERNEL void __launch_bounds__(256) vkf_gemm_q6_k_q8_1_int(VkfGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 lx[2][BM * PF];
-    __shared__ __attribute__((aligned(16))) _Float16 ly[2][BN * PF];
-    __shared__ float ldx[2][BM];
-    __shared__ float ldw[2][BN];
-    const uint32_t r0 = blockIdx.y * BM, c0 = blockIdx.x * BN;
-    const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
-    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
-    const uint8_t *X = (const uint8_t *)a.X, *Y = (const uint8_t *)a.Y;
-    vkf_f4 acc[4][4], accs[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = accs[i][j] = vkf_f4{0, 0, 0, 0};
-    const uint32_t nk = a.K / 32;
-
-    // thread t: X row t/2 (16 q8 values), Y row t/2 (16 weights)
-    const int trow = threadIdx.x >> 1, th = threadIdx.x & 1;
-    auto load = [&](uint32_t kb, vkf_h8 vx[2], vkf_h8 vy[2], float &dx, float &dw) {
-        uint32_t r = r0 + trow;
-        vx[0] = vx[1] = vkf_h8{};
-        dx = 0.0f;
-        if (r < a.R) {
-            const uint8_t *xb = X + (uint64_t)r * a.ldx + 36ull * kb;
-            dx = vkf_h2f(ld_u16(xb));
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                uint32_t w0 = ld_u32(xb + 4 + 16 * th + 8 * i), w1 = ld_u32(xb + 8 + 16 * th + 8 * i);
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    vx[i][j] = (_Float16)(int8_t)(w0 >> (8 * j));
-                    vx[i][4 + j] = (_Float16)(int8_t)(w1 >> (8 * j));
-                }
-            }
-        }
-        uint32_t c = c0 + trow;
-        vy[0] = vy[1] = vkf_h8{};
-        dw = 0.0f;
-        if (c < a.Cn) {
-            uint32_t sb = kb >> 3, j8 = kb & 7, ip = j8 >> 2, t = j8 & 3;
-            const uint8_t *b = Y + (uint64_t)c * a.ldy + 210ull * sb;
-            dw = vkf_h2f(ld_u16(b + 208));
-            int sc = (int)(int8_t)b[192 + 8 * ip + 2 * t + th];
-            const uint8_t *ql = b + 64 * ip + 32 * (t & 1) + 16 * th;
-            const uint8_t *qh = b + 128 + 32 * ip + 16 * th;
-            uint32_t sh = (t >> 1) * 4, hs = 2 * t;
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    uint32_t lo = ld_u32_a2(ql + 8 * i + 4 * q), hi = ld_u32_a2(qh + 8 * i + 4 * q);
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        int v = (int)(((lo >> (8 * j + sh)) & 0xfu) | (((hi >> (8 * j + hs)) & 3u) << 4)) - 32;
-                        vy[i][4 * q + j] = (_Float16)(sc * v);
-                    }
-                }
-            }
-        }
-    };
-    auto store = [&](int buf, const vkf_h8 vx[2], const vkf_h8 vy[2], float dx, float dw) {
-        *(vkf_h8 *)(lx[buf] + trow * PF + 16 * th) = vx[0];
-        *(vkf_h8 *)(lx[buf] + trow * PF + 16 * th + 8) = vx[1];
-        *(vkf_h8 *)(ly[buf] + trow * PF + 16 * th) = vy[0];
-        *(vkf_h8 *)(ly[buf] + trow * PF + 16 * th + 8) = vy[1];
-        if (th == 0) { ldx[buf][trow] = dx; ldw[buf][trow] = dw; }
-    };
-    vkf_h8 vx[2], vy[2];
-    float dx, dw;
-    load(0, vx, vy, dx, dw);
-    store(0, vx, vy, dx, dw);
-    __syncthreads();
-    for (uint32_t kb = 0; kb < nk; kb++) {
-        const int cur = kb & 1;
-        const bool more = kb + 1 < nk;
-        if (more) load(kb + 1, vx, vy, dx, dw);
-        vkf_h8 fa[4], fb[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) fa[i] = *(const vkf_h8 *)(lx[cur] + (wr * 64 + 16 * i + li) * PF + 8 * lg);
-#pragma unroll
-        for (int j = 0; j < 4; j++) fb[j] = *(const vkf_h8 *)(ly[cur] + (wc * 64 + 16 * j + li) * PF + 8 * lg);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float dxs[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) dxs[e] = ldx[cur][wr * 64 + 16 * i + 4 * lg + e];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                vkf_f4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], vkf_f4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 4; e++) accs[i][j][e] = fmaf(dxs[e], p[e], accs[i][j][e]);
-            }
-        }
-        if ((kb & 7) == 7) {  // super-block boundary: apply dw[n, sb]
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                float w = ldw[cur][wc * 64 + 16 * j + li];
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        acc[i][j][e] = fmaf(w, accs[i][j][e], acc[i][j][e]);
-                        accs[i][j][e] = 0.0f;
-                    }
-            }
-        }
-        if (more) store(cur ^ 1, vx, vy, dx, dw);
-        __syncthreads();
-    }
-    store_acc_f32(a, r0, c0, wr, wc, acc);
-}
