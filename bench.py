@@ -175,8 +175,8 @@ def run_suite(torch, ops, O, reps):
     xf = torch.from_numpy(np.random.default_rng(_seed(5, 1)).normal(0, 1, (M, K)).astype(np.float32)).to(dev)
     xq = ops.quantize_q8_1(xf)
     y = torch.empty((M, N), dtype=torch.float32, device=dev)
-    gemm_line("C5 Q6_K x Q8_1 prefill 512x152064x5120 (integer-exact MFMA)", 2.0 * M * N * K, INT8_PEAK_TOPS,
-              [lambda: ops.gemm_q(w, O.Q6_K, xq, N, K, out=y)])
+    gemm_line("C5 Q6_K x Q8_1 prefill 512x152064x5120 (both operands decoded to fp16, fp16 MFMA)", 2.0 * M * N * K,
+              FP16_PEAK_TFLOPS, [lambda: ops.gemm_q(w, O.Q6_K, xq, N, K, out=y)])
     del w, xf, xq, y
     torch.cuda.empty_cache()
     return out

@@ -200,3 +200,17 @@ def test_gemv_q6k_q81_dot(dev, N, K):
     y = ops.gemm_q(to_dev(w, dev), O.Q6_K, to_dev(xq, dev), N, K).cpu().numpy()
     ref = O.ref_gemv(x64, O.np_dequant(O.Q6_K, w).reshape(N, K))
     assert rel_err(y, ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("M", [5, 8, 9, 16])
+@pytest.mark.parametrize("N", [77, 3001])
+@pytest.mark.parametrize("K", [2304, 13824])
+def test_gemv_mfma_q4_k(dev, M, N, K):
+    """Q4_K x fp16 at 5 <= M <= 16 on the matrix cores: 8- and 16-row
+    activation images, every K-split width the host picks, and K = 13824,
+    which runs as several K-slice launches accumulating into y."""
+    from vkflame_amd import ops
+    w = O.gen_weight(O.Q4_K, N, K, seed_for(2, 60 + M))
+    xa, x64 = _x("f16", M, K, seed_for(2, 70 + M))
+    y = ops.gemm_q(to_dev(w, dev), O.Q4_K, to_dev(xa, dev), N, K).cpu().numpy()
+    assert _per_row_err(y, x64, w, O.Q4_K, N, K) <= TOL_F32
