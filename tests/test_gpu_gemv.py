@@ -202,15 +202,19 @@ def test_gemv_q6k_q81_dot(dev, N, K):
     assert rel_err(y, ref) <= TOL_F32
 
 
+MFMA_TYPES = [O.Q4_K, O.Q4_0, O.Q4_1]
+
+
+@pytest.mark.parametrize("qt", MFMA_TYPES, ids=[O.QNAMES[q] for q in MFMA_TYPES])
 @pytest.mark.parametrize("M", [5, 8, 9, 16])
 @pytest.mark.parametrize("N", [77, 3001])
 @pytest.mark.parametrize("K", [2304, 13824])
-def test_gemv_mfma_q4_k(dev, M, N, K):
-    """Q4_K x fp16 at 5 <= M <= 16 on the matrix cores: 8- and 16-row
-    activation images, every K-split width the host picks, and K = 13824,
-    which runs as several K-slice launches accumulating into y."""
+def test_gemv_mfma(dev, qt, M, N, K):
+    """Q4_K, Q4_0, Q4_1 x fp16 at 5 <= M <= 16 on the matrix cores: 8- and
+    16-row activation images, every K-split width the host picks, and
+    K = 13824, which runs as several K-slice launches accumulating into y."""
     from vkflame_amd import ops
-    w = O.gen_weight(O.Q4_K, N, K, seed_for(2, 60 + M))
+    w = O.gen_weight(qt, N, K, seed_for(2, 60 + M + 20 * qt))
     xa, x64 = _x("f16", M, K, seed_for(2, 70 + M))
-    y = ops.gemm_q(to_dev(w, dev), O.Q4_K, to_dev(xa, dev), N, K).cpu().numpy()
-    assert _per_row_err(y, x64, w, O.Q4_K, N, K) <= TOL_F32
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
+    assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32

@@ -31,14 +31,14 @@ constexpr int kInval = hipErrorInvalidValue;
 constexpr int kNotSup = hipErrorNotSupported;
 
 // MFMA GEMV (kernels/gemv_mfma.hip): LDS bytes of the K-split partials, and
-// the waves per 16-row tile: 4 while the tiles give most of the CUs' 16 waves
-// a share (4 tiles per workgroup), else 8 (measured faster than 16 down to
-// a few hundred tiles), 16 for very few rows.
+// the waves per 16-row tile, from a sweep on MI355X: 4 from 1.5 tiles per CU
+// up (688 and 864 tiles: 4 beats 8 by 10-20%), 8 below (320 tiles: 8 beats
+// 4 by 20%), 16 for very few rows.
 constexpr size_t kMfmaRed = 16384;
 
 static uint32_t mfma_split(uint32_t tiles, uint32_t cus) {
-    if ((uint64_t)tiles * 4 >= (uint64_t)cus * 12) return 4;
-    return (uint64_t)tiles * 8 >= (uint64_t)cus * 4 ? 8 : 16;
+    if ((uint64_t)tiles * 2 >= (uint64_t)cus * 3) return 4;
+    return (uint64_t)tiles * 3 >= cus ? 8 : 16;
 }
 
 // Kernel id of GEMV(qt, activation kind 0 fp16 / 1 fp32 / 2 Q8_1).
@@ -173,28 +173,31 @@ int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const voi
             const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_DOT_Q4_0_F16_M1 + 4 * fi + (M == 1 ? 0 : 2) + xk);
             return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * kDotWaves), a, S(stream), lds);
         }
-        // Q4_K x fp16 at 5 <= M <= 16 on the matrix cores
+        // Q4_K, Q4_0, Q4_1 x fp16 at 5 <= M <= 16 on the matrix cores
         // (kernels/gemv_mfma.hip): the activations of a K slice staged for 8
-        // or 16 rows (512 bytes per row and super-block, plus 32 of
-        // sub-block sums), next to 16 KiB of K-split partials; a K too long
-        // for LDS runs as several launches, the later ones accumulating.
-        const uint32_t mr = M <= 8 ? 8 : 16;
-        if (qt == VKF_Q4_K && M >= 5 && xk == 0 && aligned(w, 16) && (row_bytes % 16) == 0 &&
-            vkf::max_lds() >= kMfmaRed + mr * 544) {
-            const uint32_t nsb = (uint32_t)(K / 256), cap = (uint32_t)((vkf::max_lds() - kMfmaRed) / (mr * 544));
+        // or 16 rows (512 bytes per row and 256 k, plus 32 of Q4_K sub-block
+        // sums), next to 16 KiB of K-split partials; a K too long for LDS
+        // runs as several launches, the later ones accumulating.
+        const int mf = qt == VKF_Q4_K ? 0 : qt == VKF_Q4_0 ? 1 : qt == VKF_Q4_1 ? 2 : -1;
+        const uint32_t mr = M <= 8 ? 8 : 16, ga = mf == 0 ? 16 : 4;
+        const size_t per_group = (size_t)mr * (mf == 0 ? 544 : 512);
+        if (mf >= 0 && M >= 5 && xk == 0 && (K % 256) == 0 && aligned(w, ga) && (row_bytes % ga) == 0 &&
+            vkf::max_lds() >= kMfmaRed + per_group) {
+            const uint32_t nsb = (uint32_t)(K / 256), cap = (uint32_t)((vkf::max_lds() - kMfmaRed) / per_group);
             const uint32_t slices = cdiv(nsb, cap), per = cdiv(nsb, slices);
             const uint32_t cus = (uint32_t)vkf::cu_count(), tiles = cdiv(N, 16);
             const uint32_t P = mfma_split(tiles, cus);
             const uint32_t G = 16 / P, grid = cdiv(tiles, G) < cus ? cdiv(tiles, G) : cus;
+            const uint64_t group_bytes = mf == 2 ? 160 : 144;
+            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_MFMA_Q4_K_F16 + mf);
             for (uint32_t s0 = 0; s0 < nsb; s0 += per) {
                 const uint32_t n_sb = nsb - s0 < per ? nsb - s0 : per;
                 VkfGemvArgs b = a;
-                b.w = a.w + 144ull * s0;
+                b.w = a.w + group_bytes * s0;
                 b.x = (const uint16_t *)x + (uint64_t)s0 * 256;
                 b.K = n_sb * 256;
                 b.flags = (P << 8) | (a.flags & 1u) | (s0 > 0 ? 1u : 0u);
-                const int rc = vkf::launch(VKF_K_GEMV_MFMA_Q4_K_F16, dim3(grid), dim3(1024), b, S(stream),
-                                           kMfmaRed + (size_t)mr * 544 * n_sb);
+                const int rc = vkf::launch(k, dim3(grid), dim3(1024), b, S(stream), kMfmaRed + per_group * n_sb);
                 if (rc) return rc;
             }
             return 0;

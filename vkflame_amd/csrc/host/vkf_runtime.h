@@ -55,6 +55,8 @@
     X(Q6_K_Q8_1_PARTIALS, "vkf_q6_k_q8_1_partials")         \
     X(GEMV_Q6K_Q81_DOT_M1, "vkf_gemv_q6k_q81_dot_m1")      \
     X(GEMV_MFMA_Q4_K_F16, "vkf_gemv_mfma_q4_k_f16")        \
+    X(GEMV_MFMA_Q4_0_F16, "vkf_gemv_mfma_q4_0_f16")        \
+    X(GEMV_MFMA_Q4_1_F16, "vkf_gemv_mfma_q4_1_f16")        \
     /* dot-product GEMV: per format {f16, f32} x {m1, m4} */ \
     X(GEMV_DOT_Q4_0_F16_M1, "vkf_gemv_dot_q4_0_f16_m1") \
     X(GEMV_DOT_Q4_0_F32_M1, "vkf_gemv_dot_q4_0_f32_m1") \

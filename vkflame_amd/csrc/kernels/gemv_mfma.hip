@@ -1,11 +1,15 @@
-// gemv_mfma.hip — small-batch GEMV (5 <= M <= 16) of Q4_K weights on the
-// matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T, fp16 activations.
+// gemv_mfma.hip — small-batch GEMV (5 <= M <= 16) of Q4_K, Q4_0 and Q4_1
+// weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T, fp16
+// activations.
 //
 // With 5..16 activation rows the VALU dot product costs M multiply-adds per
 // weight; a 16x16x32 fp16 MFMA takes 16 weight rows x 32 k against up to 16
-// activation rows at once, so the per-weight cost is the decode only.
+// activation rows at once, so the per-weight cost is the decode only.  Work
+// is counted in groups of 256 k of a row: a Q4_K super-block (144 bytes), 8
+// Q4_0 blocks (144 bytes) or 8 Q4_1 blocks (160 bytes); a group of a 16-row
+// tile is 8 MFMA steps.
 //
-// Arithmetic.  A Q4_K weight is dall*sc*q - dmin*mn (kernels/dequant_q4_k.glsl:
+// Q4_K arithmetic.  A weight is dall*sc*q - dmin*mn (kernels/dequant_q4_k.glsl:
 // 16-58; sc, mn 6-bit per 32-element sub-block, q a nibble).  Per super-block
 // and output (m, n):
 //   y += dall * sum_k x*(sc*q)  -  dmin * sum_j mn_j * xs_j
@@ -15,58 +19,80 @@
 // MFMA whose k runs over the 8 sub-blocks: A = xs/32 as two fp16 halves
 // (hi + lo, ~22 bits) on k-slices 0 and 1, B = mn.
 //
-// Decode.  A code dword holds bytes b0..b3 (low nibble: sub-block 2il,
-// high: 2il+1).  (v & 0x000f000f) | 0x64006400 is the fp16 pair
-// (1024 + b0.lo, 1024 + b2.lo); the same with mask 0x00f000f0 gives
-// (1024 + 16*b0.hi, 1024 + 16*b2.hi), and v >> 8 the b1, b3 pairs.  One
-// packed fp16 FMA per pair, (1024 + q)*sc - 1024*sc or (1024 + 16q)*(sc/16)
-// - 64*sc, yields sc*q exactly.
+// Q4_0 / Q4_1 arithmetic.  The MFMA operand is the dequantised weight in
+// fp16, d*(q-8) (kernels/dequant_q4_0.glsl) or d*q + m (dequant_q4_1.glsl),
+// rounded once from the exact value; products and sums run in fp32.
 //
-// Loads and k order.  Lane l = 16g + i (weight row i) loads, per
-// super-block, the 16-byte header and qs bytes 16g .. +15 and 64 + 16g ..
-// +15, so that each load instruction reads 64 contiguous bytes of each of
-// the 16 rows.  Those are elements 16(g&1) .. +15 of sub-blocks
-// j = 4L + 2(g>>1) + nib (L = which load, nib = low / high nibbles).  MFMA
-// step t = 4L + 2nib + hf of the super-block takes, in k-slice g, elements
-// 16(g&1) + 8hf + {0,2,1,3,4,6,5,7} of that sub-block (the decode's order),
-// and the activations are staged to match.
+// Decode.  A code dword holds bytes b0..b3.  (v & 0x000f000f) | 0x64006400 is
+// the fp16 pair (1024 + b0.lo, 1024 + b2.lo); mask 0x00f000f0 gives
+// (1024 + 16*b0.hi, 1024 + 16*b2.hi), and v >> 8 the b1, b3 pairs.  Q4_K:
+// one packed fp16 FMA per pair, (1024 + q)*sc - 1024*sc or
+// (1024 + 16q)*(sc/16) - 64*sc, yields sc*q exactly.  Q4_0 / Q4_1: one packed
+// op makes q (or q - 8) exactly, a second applies d (and m).  A lane's 8 k of
+// a step thus come in the order 0,2,1,3,4,6,5,7, and the activations are
+// staged in that order.
+//
+// Loads and k order.  Lane l = 16g + i owns weight row i of the tile.
+//   Q4_K: per super-block the 16-byte header and qs bytes 16g .. +15 and
+//   64 + 16g .. +15 (64 contiguous bytes per row per load instruction): the
+//   elements 16(g&1) .. +15 of sub-blocks j = 4L + 2(g>>1) + nib (L = which
+//   load, nib = low / high nibbles).  Step t = 4L + 2nib + hf takes, in
+//   k-slice g, elements 16(g&1) + 8hf .. +7 of that sub-block.
+//   Q4_0 / Q4_1: the block pair 2g, 2g+1 of the group (36 or 40 contiguous
+//   bytes, 4-byte aligned).  Step t = 4blk + 2nib + hf takes, in k-slice g,
+//   elements 16nib + 8hf .. +7 of block 2g + blk (low nibbles of qs bytes
+//   8hf .. +7, or their high nibbles).
 //
 // Work split.  One 1024-thread workgroup per CU stages the activation rows in
 // LDS once, with the first weight loads already in flight.  Its 16 waves form
 // 16/P groups; a group owns a 16-row tile of W per round and its P waves
-// split the tile's super-blocks P ways (P = 4, 8 or 16 from the host, larger
+// split the tile's 256-k groups P ways (P = 4, 8 or 16 from the host, larger
 // for fewer rows, so that enough loads are in flight).  A wave issues the
-// loads of up to GM_MAXSB super-blocks, then runs 9 MFMAs per super-block;
-// the P partial 16x16 results of a group meet in LDS.  The host splits a K
-// too long for LDS into launches over K slices, the later ones accumulating
-// into y.  Accumulator: lane l holds y-tile element (activation row 4g + e,
-// weight row i).
+// loads of up to gm_maxsb groups, then runs the MFMAs; the P partial 16x16
+// results of a tile meet in LDS.  The host splits a K too long for LDS into
+// launches over K slices, the later ones accumulating into y.  Accumulator:
+// lane l holds y-tile element (activation row 4g + e, weight row i).
 #include "vkf_device.h"
 
 #define GM_WAVES 16
-#define GM_MAXSB 5   // super-blocks per wave held in registers at once
+enum { GF_Q4_K = 0, GF_Q4_0 = 1, GF_Q4_1 = 2 };
+
+// 256-k groups per wave held in registers at once (the most without spills)
+template <int F> constexpr int gm_maxsb() { return F == GF_Q4_K ? 5 : 4; }
+
+template <int F> constexpr uint32_t gm_group_bytes() { return F == GF_Q4_1 ? 160 : 144; }
+
+// k offset, within its 256-k group, of the 8 elements of MFMA step t, k-slice g
+template <int F>
+__device__ __forceinline__ uint32_t gm_k0(uint32_t t, uint32_t g) {
+    if constexpr (F == GF_Q4_K) {
+        const uint32_t j = 4 * (t >> 2) + 2 * (g >> 1) + ((t >> 1) & 1), r = 2 * (g & 1) + (t & 1);
+        return 32 * j + 8 * r;
+    } else {
+        return 64 * g + 32 * (t >> 2) + 16 * ((t >> 1) & 1) + 8 * (t & 1);
+    }
+}
 
 // LDS image, MR = M rounded up to 8 or 16 (rows M .. MR-1 repeat row M-1
 // and feed only discarded outputs):
-//   x:  for MFMA step s = 8sb + t, k-slice g, row i: 8 fp16 at
-//       ((s*4 + g)*MR + i)*16, the elements 32j + 8r .. +7 of super-block sb
-//       with j = 4(t>>2) + 2(g>>1) + ((t>>1)&1), r = 2(g&1) + (t&1), in the
-//       decode's order 0,2,1,3,4,6,5,7;
-//   xs: at K*MR*2, for super-block sb, h = 0, 1 and row i: 16 bytes at
-//       ((sb*2 + h)*MR + i)*16 holding xs/32 of sub-blocks
+//   x:  for MFMA step s = 8*group + t, k-slice g, row i: 8 fp16 at
+//       ((s*4 + g)*MR + i)*16, the elements k0 = 256*group + gm_k0(t, g) ..
+//       +7 in the decode's order 0,2,1,3,4,6,5,7;
+//   xs (Q4_K only): at K*MR*2, for super-block sb, h = 0, 1 and row i: 16
+//       bytes at ((sb*2 + h)*MR + i)*16 holding xs/32 of sub-blocks
 //       J_h = {2h, 2h+1, 4+2h, 5+2h} as 4 fp16 hi parts, then 4 lo parts;
 //   partials: 16 KiB after that.
 // Staging: direct-to-LDS loads put each 16-byte piece of x in place (piece
-// = lane of a 1 KiB load), then one pass per (row, sub-block) reorders the
-// 4 pieces' halves and writes the sub-block sum.
+// = lane of a 1 KiB load), then a pass reorders the halves of every piece
+// (and, for Q4_K, writes the sub-block sums).
+template <int F> constexpr uint32_t gm_xs_bytes_per_group(uint32_t MR) { return F == GF_Q4_K ? 32 * MR : 0; }
 
 // the x pieces of the workgroup's 1 KiB direct load c
-template <uint32_t MR>
+template <int F, uint32_t MR>
 __device__ __forceinline__ void gm_dma_x(const VkfGemvArgs &a, unsigned char *lds, uint32_t c, int lane) {
     const uint32_t P = c * 64 + lane, i = P % MR, g = (P / MR) & 3, s = P / (4 * MR);
-    const uint32_t sb = s >> 3, t = s & 7;
-    const uint32_t j = 4 * (t >> 2) + 2 * (g >> 1) + ((t >> 1) & 1), r = 2 * (g & 1) + (t & 1);
-    const _Float16 *src = (const _Float16 *)a.x + (uint64_t)(i < a.M ? i : a.M - 1) * a.ldx + sb * 256 + 32 * j + 8 * r;
+    const _Float16 *src =
+        (const _Float16 *)a.x + (uint64_t)(i < a.M ? i : a.M - 1) * a.ldx + (s >> 3) * 256 + gm_k0<F>(s & 7, g);
     // Written out (M0 = LDS base, one wait state after the M0 write) so that
     // the compiler does not track it: its waits for direct-to-LDS loads are
     // vmcnt(0) before every later LDS access, weights included.  The caller
@@ -76,9 +102,23 @@ __device__ __forceinline__ void gm_dma_x(const VkfGemvArgs &a, unsigned char *ld
                  : "memory", "m0");
 }
 
-// the reorder and sub-block sums, after the direct loads have landed
-template <uint32_t MR>
+// halves 0,1,2,3 -> 0,2,1,3 (and 4..7 likewise)
+__device__ __forceinline__ vkf_u4 gm_reorder(vkf_u4 v) {
+    return vkf_u4{__builtin_amdgcn_perm(v[1], v[0], 0x05040100u), __builtin_amdgcn_perm(v[1], v[0], 0x07060302u),
+                  __builtin_amdgcn_perm(v[3], v[2], 0x05040100u), __builtin_amdgcn_perm(v[3], v[2], 0x07060302u)};
+}
+
+// the reorder (and Q4_K's sub-block sums), after the direct loads have landed
+template <int F, uint32_t MR>
 __device__ __forceinline__ void gm_stage_pass(const VkfGemvArgs &a, unsigned char *lds) {
+    if constexpr (F != GF_Q4_K) {
+        const uint32_t pieces = (a.K / 8) * MR;
+        for (uint32_t p = threadIdx.x; p < pieces; p += blockDim.x) {
+            vkf_u4 *pc = (vkf_u4 *)(lds + p * 16);
+            *pc = gm_reorder(*pc);
+        }
+        return;
+    }
     const uint32_t items = (a.K / 32) * MR;  // (super-block, sub-block, row)
     unsigned char *xs = lds + (uint64_t)a.K * MR * 2;
     const vkf_h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
@@ -97,14 +137,12 @@ __device__ __forceinline__ void gm_stage_pass(const VkfGemvArgs &a, unsigned cha
         for (int r = 0; r < 4; r++) {
 #pragma unroll
             for (int d = 0; d < 4; d++) {
+                // (a bit_cast of the vector element itself read element 0 for
+                // every d with this compiler)
                 const uint32_t w = v[r][d];
                 f = __builtin_amdgcn_fdot2(__builtin_bit_cast(vkf_h2, w), ones, f, false);
             }
-            // halves 0,1,2,3 -> 0,2,1,3 (and 4..7 likewise)
-            *pc[r] = vkf_u4{__builtin_amdgcn_perm(v[r][1], v[r][0], 0x05040100u),
-                            __builtin_amdgcn_perm(v[r][1], v[r][0], 0x07060302u),
-                            __builtin_amdgcn_perm(v[r][3], v[r][2], 0x05040100u),
-                            __builtin_amdgcn_perm(v[r][3], v[r][2], 0x07060302u)};
+            *pc[r] = gm_reorder(v[r]);
         }
         const float fs = f * 0.03125f;
         const _Float16 hi = (_Float16)fs, lo = (_Float16)(fs - (float)hi);
@@ -115,25 +153,48 @@ __device__ __forceinline__ void gm_stage_pass(const VkfGemvArgs &a, unsigned cha
     }
 }
 
-struct GmSb {          // one lane's share of a Q4_K super-block
-    vkf_u4 hdr;        // dall, dmin, scales[12]
-    vkf_u4 q[2];       // qs bytes 16g .. +15 and 64 + 16g .. +15
+// One lane's share of a 256-k group: Q4_K header, qs 16g.. and 64+16g..;
+// Q4_0 the 36 bytes of block pair g (v[2][0] last); Q4_1 its 40 bytes
+// (v[2][0..1] last).
+struct GmSb {
+    vkf_u4 v[3];
 };
 
+template <int F>
 __device__ __forceinline__ void gm_load(const uint8_t *row, uint32_t sb, int g, GmSb &t) {
-    const uint8_t *b = row + 144ull * sb;
-    t.hdr = *(const vkf_u4 *)b;
-    t.q[0] = *(const vkf_u4 *)(b + 16 + 16 * g);
-    t.q[1] = *(const vkf_u4 *)(b + 80 + 16 * g);
+    typedef unsigned int u4a4 __attribute__((ext_vector_type(4), aligned(4)));
+    typedef unsigned int u2a4 __attribute__((ext_vector_type(2), aligned(4)));
+    const uint8_t *b = row + (uint64_t)gm_group_bytes<F>() * sb;
+    if constexpr (F == GF_Q4_K) {
+        t.v[0] = *(const vkf_u4 *)b;
+        t.v[1] = *(const vkf_u4 *)(b + 16 + 16 * g);
+        t.v[2] = *(const vkf_u4 *)(b + 80 + 16 * g);
+    } else if constexpr (F == GF_Q4_0) {
+        const uint8_t *p = b + 36 * g;
+        t.v[0] = *(const u4a4 *)p;
+        t.v[1] = *(const u4a4 *)(p + 16);
+        t.v[2][0] = *(const uint32_t *)(p + 32);
+    } else {
+        const uint8_t *p = b + 40 * g;
+        t.v[0] = *(const u4a4 *)p;
+        t.v[1] = *(const u4a4 *)(p + 16);
+        const vkf_u2 c = *(const u2a4 *)(p + 32);
+        t.v[2][0] = c[0];
+        t.v[2][1] = c[1];
+    }
 }
 
-// Loads of super-blocks s0 .. s0 + GM_MAXSB - 1, those at or past sb1
-// clamped to sb1 - 1 (loaded and not used), so that the loads form one
-// straight sequence.  sb1 >= 1.
+// Loads of groups s0 .. s0 + gm_maxsb - 1, those at or past sb1 clamped to
+// sb1 - 1 (loaded and not used), so that the loads form one straight
+// sequence.  sb1 >= 1.
+template <int F>
 __device__ __forceinline__ void gm_load_batch(const uint8_t *row, uint32_t s0, uint32_t sb1, int g, GmSb *t) {
 #pragma unroll
-    for (int u = 0; u < GM_MAXSB; u++) gm_load(row, s0 + u < sb1 ? s0 + u : sb1 - 1, g, t[u]);
+    for (int u = 0; u < gm_maxsb<F>(); u++) gm_load<F>(row, s0 + u < sb1 ? s0 + u : sb1 - 1, g, t[u]);
 }
+
+// load instructions gm_load issues
+template <int F> constexpr int gm_loads_per_group() { return 3; }
 
 __device__ __forceinline__ vkf_h2 gm_h2(uint32_t u) { return __builtin_bit_cast(vkf_h2, u); }
 __device__ __forceinline__ uint32_t gm_u(vkf_h2 h) { return __builtin_bit_cast(uint32_t, h); }
@@ -146,25 +207,55 @@ __device__ __forceinline__ uint32_t gm_and_or(uint32_t v, uint32_t mask, uint32_
     return r;
 }
 
-// sc*q for 8 elements of a sub-block held in low nibbles (HI = 0) or high
-// nibbles (HI = 1) of a lane's code dwords d0, d1 and their >> 8 shifts
-// t0, t1; s, n = the sub-block's (sc, -1024*sc) or (sc/16, -64*sc);
+// (1024 + q) or (1024 + 16q) fp16 pairs of 8 elements held in the low (HI = 0)
+// or high (HI = 1) nibbles of code dwords d0, d1 and their >> 8 shifts t0, t1;
 // c64 = 0x64006400
+template <int HI>
+__device__ __forceinline__ void gm_nibbles(uint32_t d0, uint32_t t0, uint32_t d1, uint32_t t1, uint32_t c64,
+                                           vkf_h2 h[4]) {
+    const uint32_t mask = HI ? 0x00f000f0u : 0x000f000fu;
+    h[0] = gm_h2(gm_and_or(d0, mask, c64));
+    h[1] = gm_h2(gm_and_or(t0, mask, c64));
+    h[2] = gm_h2(gm_and_or(d1, mask, c64));
+    h[3] = gm_h2(gm_and_or(t1, mask, c64));
+}
+
+// Q4_K: sc*q; s, n = the sub-block's (sc, -1024*sc) or (sc/16, -64*sc)
 template <int HI>
 __device__ __forceinline__ vkf_h8 gm_decode(uint32_t d0, uint32_t t0, uint32_t d1, uint32_t t1, _Float16 s,
                                             _Float16 n, uint32_t c64) {
-    const uint32_t mask = HI ? 0x00f000f0u : 0x000f000fu;
+    vkf_h2 h[4];
+    gm_nibbles<HI>(d0, t0, d1, t1, c64, h);
     const vkf_h2 s2 = {s, s}, n2 = {n, n};
     vkf_u4 r;
-    r[0] = gm_u(__builtin_elementwise_fma(gm_h2(gm_and_or(d0, mask, c64)), s2, n2));
-    r[1] = gm_u(__builtin_elementwise_fma(gm_h2(gm_and_or(t0, mask, c64)), s2, n2));
-    r[2] = gm_u(__builtin_elementwise_fma(gm_h2(gm_and_or(d1, mask, c64)), s2, n2));
-    r[3] = gm_u(__builtin_elementwise_fma(gm_h2(gm_and_or(t1, mask, c64)), s2, n2));
+#pragma unroll
+    for (int p = 0; p < 4; p++) r[p] = gm_u(__builtin_elementwise_fma(h[p], s2, n2));
     return __builtin_bit_cast(vkf_h8, r);
 }
 
-template <uint32_t MR>
-__device__ __forceinline__ void gemv_mfma_q4k(const VkfGemvArgs &a, unsigned char *smem) {
+// Q4_0 (d*(q - 8)) or Q4_1 (d*q + m) weights of 8 elements; d, m fp16
+template <int F, int HI>
+__device__ __forceinline__ vkf_h8 gm_decode_w(uint32_t d0, uint32_t d1, _Float16 d, _Float16 m, uint32_t c64) {
+    vkf_h2 h[4];
+    gm_nibbles<HI>(d0, d0 >> 8, d1, d1 >> 8, c64, h);
+    // (1024 + q) - off or (1024 + 16q)/16 - off: q - 8 (Q4_0) or q (Q4_1)
+    const _Float16 sc = HI ? (_Float16)0.0625f : (_Float16)1.0f;
+    const _Float16 of = F == GF_Q4_0 ? (HI ? (_Float16)-72.0f : (_Float16)-1032.0f)
+                                     : (HI ? (_Float16)-64.0f : (_Float16)-1024.0f);
+    const vkf_h2 sc2 = {sc, sc}, of2 = {of, of}, d2 = {d, d}, m2 = {m, m};
+    vkf_u4 r;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const vkf_h2 q = __builtin_elementwise_fma(h[p], sc2, of2);
+        r[p] = gm_u(F == GF_Q4_0 ? q * d2 : __builtin_elementwise_fma(q, d2, m2));
+    }
+    return __builtin_bit_cast(vkf_h8, r);
+}
+
+__device__ __forceinline__ _Float16 gm_f16(uint32_t bits) { return __builtin_bit_cast(_Float16, (uint16_t)bits); }
+
+template <int F, uint32_t MR>
+__device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *smem) {
     const uint32_t nsb = a.K / 256;
     const uint32_t P = (a.flags >> 8) & 0xffu;  // waves per tile: 4, 8 or 16
     const uint32_t G = GM_WAVES / P;            // tiles per workgroup round
@@ -173,28 +264,29 @@ __device__ __forceinline__ void gemv_mfma_q4k(const VkfGemvArgs &a, unsigned cha
     const int li = lane & 15, lg = lane >> 4;
     const uint32_t grp = wave / P, part = wave % P;
     const uint32_t ntiles = (a.N + 15) / 16;
-    const uint32_t per = (nsb + P - 1) / P;  // super-blocks per wave
+    const uint32_t per = (nsb + P - 1) / P;  // groups per wave
     const uint32_t sb0 = part * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;  // sb1 >= 1
 
     // x goes to LDS by direct loads, the first batch of weight loads right
     // behind it; vmcnt counts in order, so waiting for x leaves the weights
     // in flight.  blockIdx.x * G < ntiles: the host launches at most
     // ceil(ntiles / G) workgroups.
-    GmSb t[GM_MAXSB];
+    constexpr int MAXSB = gm_maxsb<F>();
+    GmSb t[MAXSB];
     const uint32_t nc = MR * a.K * 2 / 1024;  // 1 KiB loads of x (MR * K * 2 is a multiple of 4096)
-    for (uint32_t c = wave; c < nc; c += GM_WAVES) gm_dma_x<MR>(a, smem, c, lane);
+    for (uint32_t c = wave; c < nc; c += GM_WAVES) gm_dma_x<F, MR>(a, smem, c, lane);
     asm volatile("" ::: "memory");
     {
         const uint32_t n = (blockIdx.x * G + grp) * 16 + li;
-        gm_load_batch(a.w + (uint64_t)(n < a.N ? n : a.N - 1) * a.row_bytes, sb0, sb1, lg, t);
+        gm_load_batch<F>(a.w + (uint64_t)(n < a.N ? n : a.N - 1) * a.row_bytes, sb0, sb1, lg, t);
     }
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * GM_MAXSB) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(gm_loads_per_group<F>() * MAXSB) : "memory");
     __syncthreads();
-    gm_stage_pass<MR>(a, smem);
+    gm_stage_pass<F, MR>(a, smem);
     __syncthreads();
     bool pre = true;
     const unsigned char *xs = smem + (uint64_t)a.K * MR * 2;
-    float *red = (float *)(xs + nsb * MR * 32);  // [16 waves][64 lanes][4]
+    float *red = (float *)(xs + nsb * gm_xs_bytes_per_group<F>(MR));  // [16 waves][64 lanes][4]
 
     const uint32_t arow = li < (int)MR ? li : li & 7;  // rows >= M feed discarded outputs
     const unsigned char *xw = smem + (lg * MR + arow) * 16;  // this lane's x pieces
@@ -211,53 +303,96 @@ __device__ __forceinline__ void gemv_mfma_q4k(const VkfGemvArgs &a, unsigned cha
         const uint32_t n = tile * 16 + li;
         const uint8_t *row = a.w + (uint64_t)(n < a.N ? n : a.N - 1) * a.row_bytes;
         vkf_f4 y4 = zero;
-        for (uint32_t s0 = sb0; s0 < sb1; s0 += GM_MAXSB) {
-            if (!pre) gm_load_batch(row, s0, sb1, lg, t);
+        for (uint32_t s0 = sb0; s0 < sb1; s0 += MAXSB) {
+            if (!pre) gm_load_batch<F>(row, s0, sb1, lg, t);
             pre = false;
 #pragma unroll
-            for (int u = 0; u < GM_MAXSB; u++) {
+            for (int u = 0; u < MAXSB; u++) {
                 const uint32_t sb = s0 + u;
                 if (sb >= sb1) break;
-                const float dall = vkf_h2f(t[u].hdr[0] & 0xffffu), dmin = vkf_h2f(t[u].hdr[0] >> 16);
-                const uint32_t s0w = t[u].hdr[1], s4w = t[u].hdr[2], s8w = t[u].hdr[3];
-                const uint32_t sc[2] = {s0w & 0x3f3f3f3fu, (s8w & 0x0f0f0f0fu) | ((s0w >> 2) & 0x30303030u)};
-                const uint32_t mn[2] = {s4w & 0x3f3f3f3fu, ((s8w >> 4) & 0x0f0f0f0fu) | ((s4w >> 2) & 0x30303030u)};
-                // load L covers sub-blocks 4L + 2h (low nibbles) and 4L + 2h + 1
-                // (high): scale pairs (sc, sc'/16), (-1024 sc, -64 sc'), and
-                // the mins (mn, mn') of those sub-blocks
-                vkf_h2 S[2], Nn[2];
-                uint32_t bm[2];
+                const unsigned char *xg = xw + sb * (32 * MR * 16);  // step 8sb
+                if constexpr (F == GF_Q4_K) {
+                    const vkf_u4 hdr = t[u].v[0];
+                    const float dall = vkf_h2f(hdr[0] & 0xffffu), dmin = vkf_h2f(hdr[0] >> 16);
+                    const uint32_t s0w = hdr[1], s4w = hdr[2], s8w = hdr[3];
+                    const uint32_t sc[2] = {s0w & 0x3f3f3f3fu, (s8w & 0x0f0f0f0fu) | ((s0w >> 2) & 0x30303030u)};
+                    const uint32_t mn[2] = {s4w & 0x3f3f3f3fu,
+                                            ((s8w >> 4) & 0x0f0f0f0fu) | ((s4w >> 2) & 0x30303030u)};
+                    // load L covers sub-blocks 4L + 2h (low nibbles) and 4L + 2h + 1
+                    // (high): scale pairs (sc, sc'/16), (-1024 sc, -64 sc'), and
+                    // the mins (mn, mn') of those sub-blocks
+                    vkf_h2 S[2], Nn[2];
+                    uint32_t bm[2];
 #pragma unroll
-                for (int L = 0; L < 2; L++) {
-                    S[L] = __builtin_elementwise_fma(gm_h2(__builtin_amdgcn_perm(0x64646464u, sc[L], sel)), one16, off);
-                    Nn[L] = S[L] * m1024;
-                    bm[L] = gm_u(gm_h2(__builtin_amdgcn_perm(0x64646464u, mn[L], sel)) + m1024);
-                }
-                vkf_f4 acc = zero;
-#pragma unroll
-                for (int L = 0; L < 2; L++)
-#pragma unroll
-                    for (int hf = 0; hf < 2; hf++) {
-                        const uint32_t d0 = t[u].q[L][2 * hf], d1 = t[u].q[L][2 * hf + 1], e0 = d0 >> 8, e1 = d1 >> 8;
-                        // MFMA steps 8sb + 4L + hf (low nibbles) and 8sb + 4L + 2 + hf (high)
-                        const unsigned char *xp = xw + sb * (32 * MR * 16) + (4 * L + hf) * (4 * MR * 16);
-                        const vkf_h8 xl = *(const vkf_h8 *)xp;
-                        const vkf_h8 xh = *(const vkf_h8 *)(xp + 2 * (4 * MR * 16));
-                        const vkf_h8 bl = gm_decode<0>(d0, e0, d1, e1, S[L][0], Nn[L][0], c64);
-                        const vkf_h8 bh = gm_decode<1>(d0, e0, d1, e1, S[L][1], Nn[L][1], c64);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, acc, 0, 0, 0);
+                    for (int L = 0; L < 2; L++) {
+                        S[L] = __builtin_elementwise_fma(gm_h2(__builtin_amdgcn_perm(0x64646464u, sc[L], sel)), one16,
+                                                         off);
+                        Nn[L] = S[L] * m1024;
+                        bm[L] = gm_u(gm_h2(__builtin_amdgcn_perm(0x64646464u, mn[L], sel)) + m1024);
                     }
-                // min term: even k-slices carry xs hi and lo of the lane pair's 4
-                // sub-blocks, odd ones zero
-                vkf_h8 xm = {};
-                if ((lg & 1) == 0) xm = *(const vkf_h8 *)(xsw + sb * (2 * MR * 16));
-                const vkf_u4 bmin = {bm[0], bm[1], bm[0], bm[1]};
-                const vkf_f4 am = __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, __builtin_bit_cast(vkf_h8, bmin), zero,
-                                                                          0, 0, 0);
-                const float dm32 = -32.0f * dmin;
+                    vkf_f4 acc = zero;
 #pragma unroll
-                for (int e = 0; e < 4; e++) y4[e] = fmaf(dm32, am[e], fmaf(dall, acc[e], y4[e]));
+                    for (int L = 0; L < 2; L++)
+#pragma unroll
+                        for (int hf = 0; hf < 2; hf++) {
+                            const vkf_u4 q = t[u].v[1 + L];
+                            const uint32_t d0 = q[2 * hf], d1 = q[2 * hf + 1], e0 = d0 >> 8, e1 = d1 >> 8;
+                            // MFMA steps 8sb + 4L + hf (low nibbles) and 8sb + 4L + 2 + hf (high)
+                            const unsigned char *xp = xg + (4 * L + hf) * (4 * MR * 16);
+                            const vkf_h8 xl = *(const vkf_h8 *)xp;
+                            const vkf_h8 xh = *(const vkf_h8 *)(xp + 2 * (4 * MR * 16));
+                            const vkf_h8 bl = gm_decode<0>(d0, e0, d1, e1, S[L][0], Nn[L][0], c64);
+                            const vkf_h8 bh = gm_decode<1>(d0, e0, d1, e1, S[L][1], Nn[L][1], c64);
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, acc, 0, 0, 0);
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, acc, 0, 0, 0);
+                        }
+                    // min term: even k-slices carry xs hi and lo of the lane pair's 4
+                    // sub-blocks, odd ones zero
+                    vkf_h8 xm = {};
+                    if ((lg & 1) == 0) xm = *(const vkf_h8 *)(xsw + sb * (2 * MR * 16));
+                    const vkf_u4 bmin = {bm[0], bm[1], bm[0], bm[1]};
+                    const vkf_f4 am =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, __builtin_bit_cast(vkf_h8, bmin), zero, 0, 0, 0);
+                    const float dm32 = -32.0f * dmin;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) y4[e] = fmaf(dm32, am[e], fmaf(dall, acc[e], y4[e]));
+                } else {
+                    // block pair 2g, 2g+1: code dwords and (d, m) of each block
+                    const vkf_u4 w0 = t[u].v[0], w1 = t[u].v[1];
+                    uint32_t q[2][4], dm[2];
+                    if constexpr (F == GF_Q4_0) {
+                        // 18-byte blocks: block 0 = bytes 0..17 (qs from byte 2),
+                        // block 1 = bytes 18..35 (qs from byte 20, aligned)
+                        const uint32_t w[5] = {w0[0], w0[1], w0[2], w0[3], w1[0]};
+#pragma unroll
+                        for (int j = 0; j < 4; j++) q[0][j] = __builtin_amdgcn_alignbyte(w[j + 1], w[j], 2);
+                        q[1][0] = w1[1]; q[1][1] = w1[2]; q[1][2] = w1[3]; q[1][3] = t[u].v[2][0];
+                        dm[0] = w0[0] & 0xffffu;
+                        dm[1] = w1[0] >> 16;
+                    } else {
+                        // 20-byte blocks: (d, m), 16 bytes of qs
+                        q[0][0] = w0[1]; q[0][1] = w0[2]; q[0][2] = w0[3]; q[0][3] = w1[0];
+                        q[1][0] = w1[2]; q[1][1] = w1[3]; q[1][2] = t[u].v[2][0]; q[1][3] = t[u].v[2][1];
+                        dm[0] = w0[0];
+                        dm[1] = w1[1];
+                    }
+#pragma unroll
+                    for (int blk = 0; blk < 2; blk++) {
+                        const _Float16 d = gm_f16(dm[blk] & 0xffffu), m = gm_f16(dm[blk] >> 16);
+#pragma unroll
+                        for (int hf = 0; hf < 2; hf++) {
+                            const uint32_t d0 = q[blk][2 * hf], d1 = q[blk][2 * hf + 1];
+                            // steps 4blk + hf (low nibbles) and 4blk + 2 + hf (high)
+                            const unsigned char *xp = xg + (4 * blk + hf) * (4 * MR * 16);
+                            const vkf_h8 xl = *(const vkf_h8 *)xp;
+                            const vkf_h8 xh = *(const vkf_h8 *)(xp + 2 * (4 * MR * 16));
+                            const vkf_h8 bl = gm_decode_w<F, 0>(d0, d1, d, m, c64);
+                            const vkf_h8 bh = gm_decode_w<F, 1>(d0, d1, d, m, c64);
+                            y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, y4, 0, 0, 0);
+                            y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, y4, 0, 0, 0);
+                        }
+                    }
+                }
             }
         }
         // K-split partials: waves of the group meet in LDS
@@ -283,8 +418,13 @@ __device__ __forceinline__ void gemv_mfma_q4k(const VkfGemvArgs &a, unsigned cha
     }
 }
 
-VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_k_f16(VkfGemvArgs a) {
+template <int F>
+__device__ __forceinline__ void gemv_mfma_entry(const VkfGemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    if (a.M <= 8) gemv_mfma_q4k<8>(a, smem);
-    else gemv_mfma_q4k<16>(a, smem);
+    if (a.M <= 8) gemv_mfma<F, 8>(a, smem);
+    else gemv_mfma<F, 16>(a, smem);
 }
+
+VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_k_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_K>(a); }
+VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_0_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_0>(a); }
+VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_1_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_1>(a); }
