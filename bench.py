@@ -156,7 +156,7 @@ def run_suite(torch, ops, O, reps):
     w = torch.from_numpy(O.gen_weight(O.Q4_K, N, K, _seed(3))).to(dev)
     x = torch.from_numpy(np.random.default_rng(_seed(3, 512)).normal(0, 1, (M, K)).astype(np.float16)).to(dev)
     y = torch.empty((M, N), dtype=torch.float32, device=dev)
-    gemm_line("C3 Q4_K prefill 512x13824x5120 (dequant->LDS fp16 MFMA)", 2.0 * M * N * K, FP16_PEAK_TFLOPS,
+    gemm_line("C3 Q4_K prefill 512x13824x5120 (weights decoded to fp16 between MFMA steps)", 2.0 * M * N * K, FP16_PEAK_TFLOPS,
               [lambda: ops.gemm_q(w, O.Q4_K, x, N, K, out=y)] * 4)
     del w, x, y
     # C4 int8 linear
