@@ -316,8 +316,8 @@ __device__ __forceinline__ void gemm_mainloop_dma(const VkfGemmArgs &a, uint32_t
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t off = (4 * wave + j) * 8 * 128;
-            __builtin_amdgcn_global_load_lds(gx[j] + (uint64_t)kt * 128, (__attribute__((address_space(3))) void *)(sx + off), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(gy[j] + (uint64_t)kt * 128, (__attribute__((address_space(3))) void *)(sy + off), 16, 0, 0);
+            vkf_load_lds16(gx[j] + (uint64_t)kt * 128, sx + off);
+            vkf_load_lds16(gy[j] + (uint64_t)kt * 128, sy + off);
         }
     };
 #pragma unroll
@@ -657,9 +657,7 @@ __device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_
         uint8_t *sx = smem + stage * 32768;
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            __builtin_amdgcn_global_load_lds(gx[j] + (uint64_t)kt * 128,
-                                             (__attribute__((address_space(3))) void *)(sx + (4 * wave + j) * 1024),
-                                             16, 0, 0);
+            vkf_load_lds16(gx[j] + (uint64_t)kt * 128, sx + (4 * wave + j) * 1024);
     };
     const uint32_t yr = threadIdx.x >> 1, yh = threadIdx.x & 1;
     auto store_y = [&](uint32_t stage, const TileRegs &t) {

@@ -93,13 +93,7 @@ __device__ __forceinline__ void gm_dma_x(const VkfGemvArgs &a, unsigned char *ld
     const uint32_t P = c * 64 + lane, i = P % MR, g = (P / MR) & 3, s = P / (4 * MR);
     const _Float16 *src =
         (const _Float16 *)a.x + (uint64_t)(i < a.M ? i : a.M - 1) * a.ldx + (s >> 3) * 256 + gm_k0<F>(s & 7, g);
-    // Written out (M0 = LDS base, one wait state after the M0 write) so that
-    // the compiler does not track it: its waits for direct-to-LDS loads are
-    // vmcnt(0) before every later LDS access, weights included.  The caller
-    // waits for it with s_waitcnt vmcnt.
-    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)(lds + c * 1024);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base)
-                 : "memory", "m0");
+    vkf_load_lds16(src, lds + c * 1024);
 }
 
 // halves 0,1,2,3 -> 0,2,1,3 (and 4..7 likewise)

@@ -204,6 +204,21 @@ template <> __device__ __forceinline__ void decode8<VKF_Q6_K>(const uint8_t *b, 
     }
 }
 
+// ---- direct-to-LDS load: each lane's 16 bytes at src go to LDS byte
+// lds + 16 * lane (lds wave-uniform) ----
+// Written out (M0 = LDS base, one wait state after the M0 write) so that the
+// compiler does not track it: its own waits for direct-to-LDS loads are
+// vmcnt(0) before every later LDS access and barrier, which would also wait
+// for every later global load.  The caller waits with s_waitcnt vmcnt(N).
+// M0 is named as clobbered; the kernels that use this hold nothing else in
+// M0 (checked in their ISA: every M0 write is this one).
+__device__ __forceinline__ void vkf_load_lds16(const void *src, const void *lds) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base)
+                 : "memory", "m0");
+}
+
 // ---- wavefront reductions (64 lanes) ----
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
