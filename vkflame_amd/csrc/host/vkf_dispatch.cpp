@@ -162,26 +162,17 @@ int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const voi
         if (xk == 1 && (!aligned(x, 16) || (ldx % 4) != 0)) return kInval;
         VkfGemvArgs a{(const uint8_t *)w, x, y, row_bytes, (uint64_t)ldx, (uint64_t)ldy,
                       (uint32_t)M, (uint32_t)N, (uint32_t)K, 0u};
-        const int fi = dot_format(qt);
-        const size_t lds = M == 1 ? kDotLdsM1 : kDotLdsM4;
-        if (fi >= 0 && M <= 4 && xk != 2 && (K % 64) == 0 && K <= kDotMaxK && lds <= vkf::max_lds() &&
-            aligned(w, kDotAlign[fi]) && (row_bytes % kDotAlign[fi]) == 0) {
-            const uint32_t rpl = M == 1 ? 1 : 2, cus = (uint32_t)vkf::cu_count();
-            const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 64), rpl, cus * kDotWaves);
-            const uint32_t tiles = cdiv(N, (64 / seg) * rpl);
-            a.flags |= seg << 8;
-            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_DOT_Q4_0_F16_M1 + 4 * fi + (M == 1 ? 0 : 2) + xk);
-            return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * kDotWaves), a, S(stream), lds);
-        }
-        // Q4_K, Q4_0, Q4_1 x fp16 at 5 <= M <= 16 on the matrix cores
-        // (kernels/gemv_mfma.hip): the activations of a K slice staged for 8
-        // or 16 rows (512 bytes per row and 256 k, plus 32 of Q4_K sub-block
-        // sums), next to 16 KiB of K-split partials; a K too long for LDS
-        // runs as several launches, the later ones accumulating.
+        // Q4_K, Q4_0, Q4_1 x fp16 at 2 <= M <= 16 on the matrix cores
+        // (kernels/gemv_mfma.hip; faster than the dot GEMV from M = 2 up,
+        // e.g. Q4_0 11008x4096 M=4 13.2 vs 16.9 us on MI355X): the
+        // activations of a K slice staged for 8 or 16 rows (512 bytes per
+        // row and 256 k, plus 32 of Q4_K sub-block sums), next to 16 KiB of
+        // K-split partials; a K too long for LDS runs as several launches,
+        // the later ones accumulating.
         const int mf = qt == VKF_Q4_K ? 0 : qt == VKF_Q4_0 ? 1 : qt == VKF_Q4_1 ? 2 : -1;
         const uint32_t mr = M <= 8 ? 8 : 16, ga = mf == 0 ? 16 : 4;
         const size_t per_group = (size_t)mr * (mf == 0 ? 544 : 512);
-        if (mf >= 0 && M >= 5 && xk == 0 && (K % 256) == 0 && aligned(w, ga) && (row_bytes % ga) == 0 &&
+        if (mf >= 0 && M >= 2 && xk == 0 && (K % 256) == 0 && aligned(w, ga) && (row_bytes % ga) == 0 &&
             vkf::max_lds() >= kMfmaRed + per_group) {
             const uint32_t nsb = (uint32_t)(K / 256), cap = (uint32_t)((vkf::max_lds() - kMfmaRed) / per_group);
             const uint32_t slices = cdiv(nsb, cap), per = cdiv(nsb, slices);
@@ -201,6 +192,17 @@ int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const voi
                 if (rc) return rc;
             }
             return 0;
+        }
+        const int fi = dot_format(qt);
+        const size_t lds = M == 1 ? kDotLdsM1 : kDotLdsM4;
+        if (fi >= 0 && M <= 4 && xk != 2 && (K % 64) == 0 && K <= kDotMaxK && lds <= vkf::max_lds() &&
+            aligned(w, kDotAlign[fi]) && (row_bytes % kDotAlign[fi]) == 0) {
+            const uint32_t rpl = M == 1 ? 1 : 2, cus = (uint32_t)vkf::cu_count();
+            const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 64), rpl, cus * kDotWaves);
+            const uint32_t tiles = cdiv(N, (64 / seg) * rpl);
+            a.flags |= seg << 8;
+            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_DOT_Q4_0_F16_M1 + 4 * fi + (M == 1 ? 0 : 2) + xk);
+            return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * kDotWaves), a, S(stream), lds);
         }
         // Q6_K x Q8_1 at M = 1 (kernels/gemv_q6k.hip): 128-element chunks,
         // 4-byte aligned rows, an 11-plane LDS image of up to 256 chunks.

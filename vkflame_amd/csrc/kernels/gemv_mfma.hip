@@ -1,8 +1,8 @@
-// gemv_mfma.hip — small-batch GEMV (5 <= M <= 16) of Q4_K, Q4_0 and Q4_1
+// gemv_mfma.hip — small-batch GEMV (2 <= M <= 16) of Q4_K, Q4_0 and Q4_1
 // weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T, fp16
 // activations.
 //
-// With 5..16 activation rows the VALU dot product costs M multiply-adds per
+// With 2..16 activation rows the VALU dot product costs M multiply-adds per
 // weight; a 16x16x32 fp16 MFMA takes 16 weight rows x 32 k against up to 16
 // activation rows at once, so the per-weight cost is the decode only.  Work
 // is counted in groups of 256 k of a row: a Q4_K super-block (144 bytes), 8
