@@ -186,12 +186,13 @@ def test_gemv_dot_dynamic_range(dev, qt):
         assert rel_err(y[m], ref[m]) <= TOL_F32, m
 
 
-@pytest.mark.parametrize("N", [1, 77, 3001])
-@pytest.mark.parametrize("K", [2048, 4608])
+@pytest.mark.parametrize("N", [1, 77, 3001, 20011])
+@pytest.mark.parametrize("K", [2048, 4608, 5120, 6144])
 def test_gemv_q6k_q81_dot(dev, N, K):
     """The Q6_K x Q8_1 integer GEMV at M = 1 (4-byte aligned rows, chunks at
     alternating 2- and 4-byte offsets), including scales over the whole int8
-    range."""
+    range.  N and K cover every row-segment width the host picks (8..64 lanes)
+    and row tails that end 0, 4, 8 or 12 bytes into a 16-byte piece."""
     from vkflame_amd import ops
     w = O.gen_weight(O.Q6_K, N, K, seed_for(5, 10 + N % 7)).reshape(-1, 210)
     rng = np.random.default_rng(seed_for(5, 11))

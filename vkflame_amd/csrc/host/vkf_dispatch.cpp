@@ -66,7 +66,10 @@ constexpr int kDotWaves = 16;
 // for up to 256 chunks of 64 elements.
 constexpr size_t kDotLdsM1 = 8 * 4096 + 4096, kDotLdsM4 = 4 * (8 * 4096 + 4096);
 constexpr int kDotMaxK = 256 * 64;
-constexpr size_t kDotLdsQ6 = 11 * 4096;  // kernels/gemv_q6k.hip, one activation row
+// kernels/gemv_q6k.hip, one activation row: x planes + two weight buffers
+// for each of its 8 waves
+constexpr size_t kDotLdsQ6 = 11 * 4096 + 8 * 2 * 7 * 1024;
+constexpr int kQ6Waves = 8;
 int dot_format(int qt) {
     switch (qt) {
     case VKF_Q4_0: return 0;
@@ -209,10 +212,10 @@ int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const voi
         if (qt == VKF_Q6_K && xk == 2 && M == 1 && K <= 256 * 128 && aligned(w, 4) && (row_bytes % 4) == 0 &&
             kDotLdsQ6 <= vkf::max_lds()) {
             const uint32_t cus = (uint32_t)vkf::cu_count();
-            const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 128), 1, cus * kDotWaves);
+            const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 128), 1, cus * kQ6Waves);
             const uint32_t tiles = cdiv(N, 64 / seg);
             a.flags |= seg << 8;
-            return vkf::launch(VKF_K_GEMV_Q6K_Q81_DOT_M1, dim3(tiles < cus ? tiles : cus), dim3(64 * kDotWaves), a,
+            return vkf::launch(VKF_K_GEMV_Q6K_Q81_DOT_M1, dim3(tiles < cus ? tiles : cus), dim3(64 * kQ6Waves), a,
                                S(stream), kDotLdsQ6);
         }
         return vkf::launch(gemv_kernel(qt, xk), dim3(cdiv(N, 4)), dim3(256), a, S(stream));

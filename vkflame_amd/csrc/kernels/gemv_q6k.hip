@@ -18,13 +18,20 @@
 //
 // Work split as in gemv_dot.hip: one 1024-thread workgroup per CU stages the
 // activations in LDS, segments of S lanes own rows, lane p takes chunks p,
-// p+S, ..., and the segment reduces with lane shuffles.  A chunk is ~27
-// dwords of loads; a second chunk in flight per lane does not fit the 128
-// registers of a 16-wave workgroup without spilling (measured slower), so
-// the 16 waves of a CU overlap each other's loads instead.
+// p+S, ..., and the segment reduces with lane shuffles.
+//
+// Loads.  Per iteration a wave needs, for each of its 64/S rows, the S/2
+// consecutive super-blocks its lanes decode: 105*S contiguous bytes per
+// row.  The wave fetches them with direct-to-LDS 16-byte loads over
+// consecutive addresses into one of its two LDS buffers (each 128-byte line
+// requested once: a CU keeps only about 64 line requests in flight, and
+// loading each lane's chunk fields straight from memory requested ~1.45
+// lines per line of weights), then every lane reads its chunk's fields from
+// there while the next iteration's loads fill the other buffer.  Two
+// buffers per wave fit LDS for 8 waves per CU (512-thread workgroups).
 #include "vkf_device.h"
 
-#define Q6_WAVES 16
+#define Q6_WAVES 8
 // bytes per LDS plane: 16 per chunk; MM = 1 up to 256 chunks (K <= 32768),
 // MM = 4 up to 128 (K <= 16384)
 template <int MM> constexpr uint32_t q6_plane_bytes() { return MM == 1 ? 4096 : 2048; }
@@ -71,10 +78,11 @@ struct Q6Raw {
     uint32_t ql[17], qh[9], sc[3], d;
 };
 
-__device__ __forceinline__ void q6_load(const uint8_t *row, uint32_t c, Q6Raw &r) {
-    const uint32_t sb = c >> 1, ip = c & 1;
-    const uint32_t base = 210u * sb - 2u * (sb & 1);  // 4-byte aligned
-    const uint8_t *p = row + base;
+// fields of chunk (local super-block lsb, half ip) from a row region that
+// starts 4-byte aligned
+__device__ __forceinline__ void q6_load(const uint8_t *region, uint32_t lsb, uint32_t ip, Q6Raw &r) {
+    const uint32_t base = 210u * lsb - 2u * (lsb & 1);  // 4-byte aligned
+    const uint8_t *p = region + base;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const vkf_u4 v = *(const vkf_u4a4 *)(p + 64 * ip + 16 * k);
@@ -89,8 +97,8 @@ __device__ __forceinline__ void q6_load(const uint8_t *row, uint32_t c, Q6Raw &r
     r.qh[8] = *(const uint32_t *)(p + 128 + 32 * ip + 32);
     r.sc[0] = *(const uint32_t *)(p + 192 + 8 * ip);
     r.sc[1] = *(const uint32_t *)(p + 196 + 8 * ip);
-    r.sc[2] = *(const uint32_t *)(p + ((sb & 1) ? 200 + 8 * ip : 196 + 8 * ip));
-    r.d = *(const uint16_t *)(row + 210u * sb + 208);
+    r.sc[2] = *(const uint32_t *)(p + ((lsb & 1) ? 200 + 8 * ip : 196 + 8 * ip));
+    r.d = *(const uint16_t *)(region + 210u * lsb + 208);
 }
 
 // sum over the chunk for activation row m: d_w * sum_t dx(t) * Q_t
@@ -135,19 +143,27 @@ __device__ __forceinline__ float q6_chunk(const Q6Raw &r, uint32_t sh, const uns
     return dw * acc;
 }
 
+// Per-wave LDS buffers: two of 64/S rows x PR 16-byte pieces each, PR =
+// ceil(105*S/16) (at most 424 pieces, S = 8), room for all 7 x 64 slots.
+#define Q6_NLD 7  // direct loads per lane per iteration (7 x 64 >= 424)
+#define Q6_WBUF (Q6_NLD * 64 * 16)
+
 // flags bit 0: y += instead of y =; bits 8..15: S (lanes per row segment,
-// a power of two 8..64).  Dynamic LDS: MM * 11 * q6_plane_bytes<MM>().
-template <int MM>
-__device__ __forceinline__ void gemv_q6k_q81(const VkfGemvArgs &a) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+// a power of two 8..64).  Dynamic LDS: MM * 11 * q6_plane_bytes<MM>() +
+// Q6_WAVES * 2 * Q6_WBUF.  row_bytes % 4 == 0 and K >= 256 (host).
+template <int MM, uint32_t S>
+__device__ __forceinline__ void gemv_q6k_q81(const VkfGemvArgs &a, unsigned char *smem) {
     const uint32_t C = a.K / 128, M = a.M, nkb = a.K / 32;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t S = (a.flags >> 8) & 0xffu;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t seg = lane / S, p = lane & (S - 1);
-    const uint32_t TR = 64 / S;  // rows per wave tile
+    constexpr uint32_t TR = 64 / S;  // rows per wave tile
+    constexpr uint32_t PR = (105 * S + 15) / 16, NP = TR * PR;
     const uint32_t ntiles = (a.N + TR - 1) / TR;
     const uint32_t iters = (C + S - 1) / S;
     const uint32_t tstep = gridDim.x * Q6_WAVES;
+    unsigned char *wb = smem + MM * 11 * q6_plane_bytes<MM>() + wave * 2 * Q6_WBUF;
+    const uint32_t last = (uint32_t)a.row_bytes - 16;  // last 16-byte piece of a row (row_bytes % 4 == 0)
 
     for (uint32_t i = threadIdx.x; i < M * nkb; i += blockDim.x) {
         const uint32_t m = i / nkb;
@@ -156,19 +172,71 @@ __device__ __forceinline__ void gemv_q6k_q81(const VkfGemvArgs &a) {
     __syncthreads();
 
     for (uint32_t tile = wave * gridDim.x + blockIdx.x; tile < ntiles; tile += tstep) {
-        const uint32_t n = tile * TR + seg;
-        const uint8_t *row = a.w + (uint64_t)(n < a.N ? n : 0) * a.row_bytes;
+        // piece P = 64j + lane of an iteration: row P / PR of the tile, bytes
+        // 16 * (P % PR) of that row's region, to LDS byte 16P of the buffer
+        // (slots past NP fetch a valid piece into the unused buffer tail)
+        // The last iteration's region may end inside a 16-byte piece (rows are
+        // 210*K/256 bytes, a multiple of 4): that piece is fetched from the
+        // row's last 16 bytes (shifted), and its rem = 4, 8 or 12 valid bytes
+        // are loaded again into registers (3 dword loads, unused ones from a
+        // valid dummy address), to be written over it once the direct loads
+        // have landed.
+        const uint32_t rl = 105u * S * (iters - 1), tl = (uint32_t)a.row_bytes - rl, rem = tl % 16;
+        const bool straddle = rem != 0 && tl < 16 * PR;  // uniform
+        uint32_t fixp = 0xffffffffu, fixv[3] = {0, 0, 0};
+        auto issue = [&](uint32_t it) {
+            const uint32_t r0 = 105u * S * it;  // region start within the row
+            unsigned char *buf = wb + (it & 1) * Q6_WBUF;
+            // this wave's reads of the buffer (two iterations ago) are done
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int j = 0; j < Q6_NLD; j++) {
+                const uint32_t P = 64 * j + lane, pp = P < NP ? P : NP - 1, rr = pp / PR;
+                const uint32_t nn = tile * TR + rr < a.N ? tile * TR + rr : a.N - 1;
+                const uint32_t off = r0 + 16 * (pp - rr * PR);
+                vkf_load_lds16(a.w + (uint64_t)nn * a.row_bytes + (off < last ? off : last), buf + 64 * j * 16);
+            }
+            if (it == iters - 1 && straddle) {
+                // piece tl/16 of each row: at most one per lane (PR is not a
+                // multiple of 64 and a tile has fewer than 64 rows)
+                const uint8_t *fa = a.w;  // a valid address for lanes without one
+                fixp = 0xffffffffu;
+#pragma unroll
+                for (int j = 0; j < Q6_NLD; j++) {
+                    const uint32_t P = 64 * j + lane, rr = P / PR;
+                    if (rr < TR && P - rr * PR == tl / 16) {
+                        const uint32_t nn = tile * TR + rr < a.N ? tile * TR + rr : a.N - 1;
+                        fa = a.w + (uint64_t)nn * a.row_bytes + rl + (tl & ~15u);
+                        fixp = P;
+                    }
+                }
+#pragma unroll
+                for (int d = 0; d < 3; d++) fixv[d] = *(const uint32_t *)(fa + (4 * d < rem ? 4 * d : 0));
+            }
+        };
         float acc[MM];
 #pragma unroll
         for (int m = 0; m < MM; m++) acc[m] = 0.0f;
-        // one chunk in flight per lane; the 16 waves of a CU overlap each
-        // other's loads
+        issue(0);
         for (uint32_t it = 0; it < iters; it++) {
+            if (it + 1 < iters) {  // wave-uniform
+                issue(it + 1);
+                if (it + 2 == iters && straddle) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(Q6_NLD + 3) : "memory");
+                else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(Q6_NLD) : "memory");
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            unsigned char *buf = wb + (it & 1) * Q6_WBUF;
+            if (it == iters - 1 && straddle && fixp != 0xffffffffu) {
+#pragma unroll
+                for (int d = 0; d < 3; d++)
+                    if (4 * d < rem) *(uint32_t *)(buf + 16 * fixp + 4 * d) = fixv[d];
+            }
             const uint32_t c = p + it * S;
             if (c < C) {
                 Q6Raw r;
-                q6_load(row, c, r);
-                const uint32_t sh = 2u * ((c >> 1) & 1u);
+                q6_load(buf + seg * PR * 16, p >> 1, p & 1, r);
+                const uint32_t sh = 2u * ((p >> 1) & 1u);  // super-block c/2 = S*it/2 + p/2, S*it/2 even
 #pragma unroll
                 for (int m = 0; m < MM; m++)
                     if (MM == 1 || m < (int)M) acc[m] += q6_chunk<MM>(r, sh, smem, m, c);
@@ -178,12 +246,20 @@ __device__ __forceinline__ void gemv_q6k_q81(const VkfGemvArgs &a) {
         for (int m = 0; m < MM; m++) {
             float v = acc[m];
             for (uint32_t o = S >> 1; o > 0; o >>= 1) v += __shfl_xor(v, (int)o, 64);
-            if (p == 0 && m < (int)M && n < a.N) {
-                float *yp = a.y + (uint64_t)m * a.ldy + n;
+            if (p == 0 && m < (int)M && tile * TR + seg < a.N) {
+                float *yp = a.y + (uint64_t)m * a.ldy + tile * TR + seg;
                 *yp = (a.flags & 1u) ? *yp + v : v;
             }
         }
     }
 }
 
-VKF_KERNEL void __launch_bounds__(64 * Q6_WAVES) vkf_gemv_q6k_q81_dot_m1(VkfGemvArgs a) { gemv_q6k_q81<1>(a); }
+VKF_KERNEL void __launch_bounds__(64 * Q6_WAVES) vkf_gemv_q6k_q81_dot_m1(VkfGemvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    switch ((a.flags >> 8) & 0xffu) {
+    case 8: gemv_q6k_q81<1, 8>(a, smem); break;
+    case 16: gemv_q6k_q81<1, 16>(a, smem); break;
+    case 32: gemv_q6k_q81<1, 32>(a, smem); break;
+    default: gemv_q6k_q81<1, 64>(a, smem); break;
+    }
+}
