@@ -220,3 +220,22 @@ def test_gemv_mfma(dev, qt, M, N, K):
     xa, x64 = _x("f16", M, K, seed_for(2, 70 + M))
     y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
     assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32
+
+
+@pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_1, O.Q4_K], ids=["q4_0", "q4_1", "q4_k"])
+@pytest.mark.parametrize("kind", ["f16", "f32"])
+@pytest.mark.parametrize("NK", [(77, 1600), (77, 1664), (77, 1728), (3001, 4096), (100003, 2624)],
+                         ids=["77x1600", "77x1664", "77x1728", "3001x4096", "100003x2624"])
+def test_gemv_dot_lds_tails(dev, qt, kind, NK):
+    """M = 1 through LDS: row regions that end 4, 8 or 12 bytes into a
+    16-byte piece (Q4_0 / Q4_1 rows of 25..27 chunks; on the large N in the
+    middle of a multi-iteration row walk), checked on a spread of rows."""
+    from vkflame_amd import ops
+    N, K = NK
+    if qt == O.Q4_K and K % 256:
+        pytest.skip("Q4_K rows are whole 256-element super-blocks")
+    w = O.gen_weight(qt, N, K, seed_for(2, 80 + qt))
+    xa, x64 = _x(kind, 1, K, seed_for(2, 81))
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
+    rows = np.unique(np.concatenate([np.arange(0, N, max(1, N // 150)), [N - 1]]))
+    assert _rows_check(y, x64, w, qt, K, rows) <= TOL_F32

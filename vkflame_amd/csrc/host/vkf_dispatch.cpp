@@ -66,6 +66,8 @@ constexpr int kDotWaves = 16;
 // for up to 256 chunks of 64 elements.
 constexpr size_t kDotLdsM1 = 8 * 4096 + 4096, kDotLdsM4 = 4 * (8 * 4096 + 4096);
 constexpr int kDotMaxK = 256 * 64;
+// M = 1 through LDS: the activations plus two 3 KiB weight buffers per wave
+constexpr size_t kDotLdsL = kDotLdsM1 + 16 * 2 * 3 * 1024;
 // kernels/gemv_q6k.hip, one activation row: x planes + two weight buffers
 // for each of its 8 waves
 constexpr size_t kDotLdsQ6 = 11 * 4096 + 8 * 2 * 7 * 1024;
@@ -197,6 +199,19 @@ int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const voi
             return 0;
         }
         const int fi = dot_format(qt);
+        // M = 1, Q4_0 / Q4_1 / Q4_K: the dot GEMV with the weights fetched
+        // into LDS by contiguous direct loads (kernels/gemv_dot.hip
+        // gemv_dot_lds): two 3 KiB buffers per wave next to the activations
+        const int li = qt == VKF_Q4_0 ? 0 : qt == VKF_Q4_1 ? 1 : qt == VKF_Q4_K ? 2 : -1;
+        if (li >= 0 && M == 1 && xk != 2 && (K % 64) == 0 && K <= kDotMaxK && kDotLdsL <= vkf::max_lds() &&
+            aligned(w, kDotAlign[fi]) && (row_bytes % kDotAlign[fi]) == 0) {
+            const uint32_t cus = (uint32_t)vkf::cu_count();
+            const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 64), 1, cus * kDotWaves);
+            const uint32_t tiles = cdiv(N, 64 / seg);
+            a.flags |= seg << 8;
+            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_DOTL_Q4_0_F16 + 2 * li + xk);
+            return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * kDotWaves), a, S(stream), kDotLdsL);
+        }
         const size_t lds = M == 1 ? kDotLdsM1 : kDotLdsM4;
         if (fi >= 0 && M <= 4 && xk != 2 && (K % 64) == 0 && K <= kDotMaxK && lds <= vkf::max_lds() &&
             aligned(w, kDotAlign[fi]) && (row_bytes % kDotAlign[fi]) == 0) {

@@ -54,6 +54,12 @@
     X(GEMV_Q6_K_Q81, "vkf_gemv_q6_k_q8_1_int")              \
     X(Q6_K_Q8_1_PARTIALS, "vkf_q6_k_q8_1_partials")         \
     X(GEMV_Q6K_Q81_DOT_M1, "vkf_gemv_q6k_q81_dot_m1")      \
+    X(GEMV_DOTL_Q4_0_F16, "vkf_gemv_dotl_q4_0_f16")        \
+    X(GEMV_DOTL_Q4_0_F32, "vkf_gemv_dotl_q4_0_f32")        \
+    X(GEMV_DOTL_Q4_1_F16, "vkf_gemv_dotl_q4_1_f16")        \
+    X(GEMV_DOTL_Q4_1_F32, "vkf_gemv_dotl_q4_1_f32")        \
+    X(GEMV_DOTL_Q4_K_F16, "vkf_gemv_dotl_q4_k_f16")        \
+    X(GEMV_DOTL_Q4_K_F32, "vkf_gemv_dotl_q4_k_f32")        \
     X(GEMV_MFMA_Q4_K_F16, "vkf_gemv_mfma_q4_k_f16")        \
     X(GEMV_MFMA_Q4_0_F16, "vkf_gemv_mfma_q4_0_f16")        \
     X(GEMV_MFMA_Q4_1_F16, "vkf_gemv_mfma_q4_1_f16")        \

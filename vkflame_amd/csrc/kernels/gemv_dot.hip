@@ -446,6 +446,145 @@ __device__ __forceinline__ void gemv_dot(const VkfGemvArgs &a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// M = 1 with the weights through LDS (Q4_0, Q4_1, Q4_K: 36- or 40-byte
+// chunks).  Per iteration a wave needs S consecutive chunks of each of its
+// 64/S rows: CB*S contiguous bytes per row, 4*CB 16-byte pieces per wave.
+// They are fetched with direct-to-LDS loads over consecutive addresses into
+// one of the wave's two LDS buffers (each 128-byte line requested once; a
+// CU keeps only ~64 line requests in flight, so fewer requests are more
+// bandwidth), and each lane reads its chunk from there while the next
+// iteration's loads fill the other buffer.  The last iteration's region may
+// end 4, 8 or 12 bytes into a piece: that piece is fetched shifted and its
+// valid bytes are loaded again into registers and written over it.
+// Dynamic LDS: dot_lds_bytes<1>() + DOT_WAVES * 2 * DOT_WBUF.
+// ---------------------------------------------------------------------------
+template <int QT> constexpr uint32_t dot_cb() { return QT == VKF_Q4_1 ? 40 : 36; }
+#define DOT_NLD 3  // direct loads per lane per iteration (3 x 64 >= 4 * 40)
+#define DOT_WBUF (DOT_NLD * 64 * 16)
+
+template <int QT, int XK, uint32_t S>
+__device__ __forceinline__ void gemv_dot_lds(const VkfGemvArgs &a, unsigned char *smem) {
+    using F = DotFmt<QT>;
+    constexpr uint32_t CB = dot_cb<QT>(), TR = 64 / S, PR = CB * S / 16, NP = TR * PR;
+    const uint32_t C = a.K / 64;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t seg = lane / S, p = lane & (S - 1);
+    const uint32_t ntiles = (a.N + TR - 1) / TR;
+    const uint32_t iters = (C + S - 1) / S;
+    const uint32_t il = p & 3;  // Q4_K: chunk c = p + S*it has c & 3 == p & 3 (S % 4 == 0)
+    const uint32_t tstep = gridDim.x * DOT_WAVES;
+    unsigned char *wb = smem + dot_lds_bytes<1>() + wave * 2 * DOT_WBUF;
+    const uint32_t last = (uint32_t)a.row_bytes - 16;  // last 16-byte piece of a row (row_bytes % 4 == 0)
+    const uint32_t rl = CB * S * (iters - 1), tl = (uint32_t)a.row_bytes - rl, rem = tl % 16;
+    const bool straddle = rem != 0 && tl < 16 * PR;  // uniform
+
+    uint32_t tile = wave * gridDim.x + blockIdx.x;
+    uint32_t fixp = 0xffffffffu, fixv[3] = {0, 0, 0};
+    auto issue = [&](uint32_t it) {
+        const uint32_t r0 = CB * S * it;  // region start within the row
+        unsigned char *buf = wb + (it & 1) * DOT_WBUF;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the buffer are done
+#pragma unroll
+        for (int j = 0; j < DOT_NLD; j++) {
+            const uint32_t P = 64 * j + lane, pp = P < NP ? P : NP - 1, rr = pp / PR;
+            const uint32_t nn = tile * TR + rr < a.N ? tile * TR + rr : a.N - 1;
+            const uint32_t off = r0 + 16 * (pp - rr * PR);
+            vkf_load_lds16(a.w + (uint64_t)nn * a.row_bytes + (off < last ? off : last), buf + 64 * j * 16);
+        }
+        if (it == iters - 1 && straddle) {
+            // piece tl/16 of each row: at most one per lane (PR < 64 or TR = 1)
+            const uint8_t *fa = a.w;  // a valid address for lanes without one
+            fixp = 0xffffffffu;
+#pragma unroll
+            for (int j = 0; j < DOT_NLD; j++) {
+                const uint32_t P = 64 * j + lane, rr = P / PR;
+                if (rr < TR && P - rr * PR == tl / 16) {
+                    const uint32_t nn = tile * TR + rr < a.N ? tile * TR + rr : a.N - 1;
+                    fa = a.w + (uint64_t)nn * a.row_bytes + rl + (tl & ~15u);
+                    fixp = P;
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < 3; d++) fixv[d] = *(const uint32_t *)(fa + (4 * d < rem ? 4 * d : 0));
+        }
+    };
+
+    // activations first (see gemv_dot), then the first tile's weights while
+    // the rest is staged
+    const uint32_t K8 = a.K / 8, items = K8, w0 = wave * 64;
+    float xv[2][8];
+    dot_load_x<XK>(a, threadIdx.x, items, K8, xv[0]);
+    dot_load_x<XK>(a, blockDim.x + threadIdx.x, items, K8, xv[1]);
+    if (w0 < items) dot_store_x<1>(smem, threadIdx.x, items, K8, xv[0]);
+    if (blockDim.x + w0 < items) dot_store_x<1>(smem, blockDim.x + threadIdx.x, items, K8, xv[1]);
+    asm volatile("" ::: "memory");
+    if (tile < ntiles) issue(0);
+    for (uint32_t i0 = 2 * blockDim.x; i0 + w0 < items; i0 += blockDim.x) {
+        dot_load_x<XK>(a, i0 + threadIdx.x, items, K8, xv[0]);
+        dot_store_x<1>(smem, i0 + threadIdx.x, items, K8, xv[0]);
+    }
+    __syncthreads();
+
+    for (; tile < ntiles; tile += tstep) {
+        float acc = 0.0f;
+        for (uint32_t it = 0; it < iters; it++) {
+            if (it + 1 < iters) {  // wave-uniform
+                issue(it + 1);
+                if (it + 2 == iters && straddle) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DOT_NLD + 3) : "memory");
+                else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DOT_NLD) : "memory");
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            unsigned char *buf = wb + (it & 1) * DOT_WBUF;
+            if (it == iters - 1 && straddle && fixp != 0xffffffffu) {
+#pragma unroll
+                for (int d = 0; d < 3; d++)
+                    if (4 * d < rem) *(uint32_t *)(buf + 16 * fixp + 4 * d) = fixv[d];
+            }
+            const uint32_t c = p + it * S;
+            if (c < C) {
+                uint32_t raw[F::NW];
+                F::load(buf + seg * PR * 16, p, raw);  // chunk p of the row's region
+                typename F::K k;
+                F::consts(raw, il, k);
+                int P[2];
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    uint32_t w[8];
+                    F::codes(raw, b, w);
+                    P[b] = group_dot(w, smem + (b * 4) * DOT_PLANE + c * 16);
+                }
+                const vkf_i4 xs = *(const vkf_i4 *)(smem + xs_offset<1>(0, c));
+                acc = F::fold(k, P[0], P[1], __int_as_float(xs[0]), xs[1], xs[2], acc);
+            }
+        }
+        const uint32_t nout = tile * TR + seg;
+        if (tile + tstep < ntiles) {  // next tile's first loads under the reduction
+            tile += tstep;
+            issue(0);
+            tile -= tstep;
+        }
+        for (uint32_t o = S >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, (int)o, 64);
+        if (p == 0 && nout < a.N) {
+            float *yp = a.y + nout;
+            *yp = (a.flags & 1u) ? *yp + acc : acc;
+        }
+    }
+}
+
+template <int QT, int XK>
+__device__ __forceinline__ void gemv_dot_lds_entry(const VkfGemvArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    switch ((a.flags >> 8) & 0xffu) {
+    case 8: gemv_dot_lds<QT, XK, 8>(a, smem); break;
+    case 16: gemv_dot_lds<QT, XK, 16>(a, smem); break;
+    case 32: gemv_dot_lds<QT, XK, 32>(a, smem); break;
+    default: gemv_dot_lds<QT, XK, 64>(a, smem); break;
+    }
+}
+
 // Chunks kept in flight per lane: two (one consumed while the other loads)
 // for one row per lane, one for two rows.
 template <int QT> constexpr int dot_depth(int rpl) { return rpl == 1 ? 2 : 1; }
@@ -469,3 +608,15 @@ VKF_GEMV_DOT(q4_0, VKF_Q4_0)
 VKF_GEMV_DOT(q4_1, VKF_Q4_1)
 VKF_GEMV_DOT(q8_0, VKF_Q8_0)
 VKF_GEMV_DOT(q4_k, VKF_Q4_K)
+
+// M = 1 through LDS: vkf_gemv_dotl_{q4_0,q4_1,q4_k}_{f16,f32}
+#define VKF_GEMV_DOTL(name, QT)                                                                         \
+    VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dotl_##name##_f16(VkfGemvArgs a) {       \
+        gemv_dot_lds_entry<QT, 0>(a);                                                                   \
+    }                                                                                                   \
+    VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dotl_##name##_f32(VkfGemvArgs a) {       \
+        gemv_dot_lds_entry<QT, 1>(a);                                                                   \
+    }
+VKF_GEMV_DOTL(q4_0, VKF_Q4_0)
+VKF_GEMV_DOTL(q4_1, VKF_Q4_1)
+VKF_GEMV_DOTL(q4_k, VKF_Q4_K)
