@@ -768,11 +768,36 @@ __device__ __forceinline__ void epilogue_tile(const VkfGemmArgs &a, uint32_t r0,
     }
 }
 
+// Workgroup -> 128 x 128 tile, XCD-aware.  Workgroups are dispatched to the
+// 8 XCDs round-robin (id % 8), each XCD with its own L2.  Columns (Y tiles)
+// are dealt to XCDs round-robin and an XCD runs all row tiles of a column
+// back to back, so a Y tile is fetched into one L2 and reused there by every
+// row tile (for the vocabulary projection, 512 x 152064 x 5120, that is 4x
+// fewer weight bytes from HBM than a row-major order).  Columns past the
+// last multiple of 8 go in plain order.
+__device__ __forceinline__ void gemm_tile_of(uint32_t &r0, uint32_t &c0) {
+    const uint32_t nc = gridDim.x, nr = gridDim.y, id = blockIdx.x + nc * blockIdx.y;
+    const uint32_t full = nc & ~7u;
+    uint32_t r, c;
+    if (id < full * nr) {
+        const uint32_t x = id & 7u, sl = id >> 3;
+        c = (sl / nr) * 8 + x;
+        r = sl % nr;
+    } else {
+        const uint32_t j = id - full * nr;
+        c = full + j / nr;
+        r = j % nr;
+    }
+    r0 = r * 128;
+    c0 = c * 128;
+}
+
 // XQT < 0: dense fp16 X, otherwise Q8_1 activation blocks (each tile value
 // fp16(dx*q)).  QT < 0: dense fp16 Y; otherwise Y holds ggml blocks of type QT.
 template <int XQT, int QT>
 __device__ __forceinline__ void gemm_f16_body(const VkfGemmArgs &a) {
-    const uint32_t r0 = blockIdx.y * 128, c0 = blockIdx.x * 128;
+    uint32_t r0, c0;
+    gemm_tile_of(r0, c0);
     vkf_f4 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -835,7 +860,8 @@ VKF_GEMM_Q_Q81(q6_k, VKF_Q6_K)
 // ---------------------------------------------------------------------------
 GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_LDS_BOTH];
-    const uint32_t r0 = blockIdx.y * 128, c0 = blockIdx.x * 128;
+    uint32_t r0, c0;
+    gemm_tile_of(r0, c0);
     vkf_i4 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
