@@ -156,7 +156,7 @@ def run_suite(torch, ops, O, reps):
     w = torch.from_numpy(O.gen_weight(O.Q4_K, N, K, _seed(3))).to(dev)
     x = torch.from_numpy(np.random.default_rng(_seed(3, 512)).normal(0, 1, (M, K)).astype(np.float16)).to(dev)
     y = torch.empty((M, N), dtype=torch.float32, device=dev)
-    gemm_line("C3 Q4_K prefill 512x13824x5120 (weights decoded to fp16 between MFMA steps)", 2.0 * M * N * K, FP16_PEAK_TFLOPS,
+    gemm_line("C3 Q4_K prefill 512x13824x5120 (weights decoded to fp16 between MFMA steps, 256-row tiles)", 2.0 * M * N * K, FP16_PEAK_TFLOPS,
               [lambda: ops.gemm_q(w, O.Q4_K, x, N, K, out=y)] * 4)
     del w, x, y
     # C4 int8 linear
@@ -175,7 +175,7 @@ def run_suite(torch, ops, O, reps):
     xf = torch.from_numpy(np.random.default_rng(_seed(5, 1)).normal(0, 1, (M, K)).astype(np.float32)).to(dev)
     xq = ops.quantize_q8_1(xf)
     y = torch.empty((M, N), dtype=torch.float32, device=dev)
-    gemm_line("C5 Q6_K x Q8_1 prefill 512x152064x5120 (both operands decoded to fp16, fp16 MFMA)", 2.0 * M * N * K,
+    gemm_line("C5 Q6_K x Q8_1 prefill 512x152064x5120 (activations decoded once to fp16, weight tiles between MFMA steps)", 2.0 * M * N * K,
               FP16_PEAK_TFLOPS, [lambda: ops.gemm_q(w, O.Q6_K, xq, N, K, out=y)])
     del w, xf, xq, y
     torch.cuda.empty_cache()

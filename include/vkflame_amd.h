@@ -100,6 +100,24 @@ int vkflame_quantize_q8_1(const float *x, void *dst, int M, int K, int64_t ldx, 
 int vkflame_dispatch_gemm_q(const void *w, int quant_type, uint64_t row_bytes, const void *x, int x_dtype,
                             int64_t ldx, float *y, int64_t ldy, int M, int N, int K, void *stream);
 
+/* vkflame_dispatch_gemm_q with a caller-supplied device workspace, in the
+ * manner of hipblasLtMatmul's workspace argument.  With Q8_1 activations,
+ * M > 16 and packed rows (ldx = K/32*36), a workspace of at least
+ * vkflame_gemm_q_workspace_bytes(x_dtype, M, K) bytes, 16-byte aligned,
+ * receives the activations decoded once to fp16(d*q) and the fp16-activation
+ * GEMM runs on them (from M = 256 with 256-row tiles); without one (NULL or
+ * too small) the GEMM decodes activation tiles itself.  Both routes multiply
+ * the same fp16 operand values.  vkflame_dispatch_gemm_q allocates the
+ * workspace stream-ordered (hipMallocAsync / hipFreeAsync) when the stream
+ * is not being captured, and goes without it under capture.  No reference
+ * counterpart as an entry point: the workspace stands for the activation
+ * temporary of the reference's mul_mat path (shim/hip_runtime_shim.cpp:1102-1172). */
+int vkflame_dispatch_gemm_q_ws(const void *w, int quant_type, uint64_t row_bytes, const void *x, int x_dtype,
+                               int64_t ldx, float *y, int64_t ldy, int M, int N, int K, void *workspace,
+                               size_t workspace_bytes, void *stream);
+/* Workspace bytes vkflame_dispatch_gemm_q_ws uses for these arguments (0: none). */
+size_t vkflame_gemm_q_workspace_bytes(int x_dtype, int M, int K);
+
 /* Integer partials of Q6_K weights w[N, K] x Q8_1 activations xq[M, K]:
  * P[(m*N + n)*(K/32) + kb] = sum over the 32 elements of block kb of
  * q8 * sc * (q6 - 32).  Exact int32; a test hook for the integer core of the

@@ -155,3 +155,62 @@ def test_config5_q6_k_q8_1_prefill(dev):
     rows = np.concatenate([[0, N - 1], np.random.default_rng(4).choice(N, 512, replace=False)])
     wd = O.np_dequant(O.Q6_K, w[rows]).reshape(len(rows), K)
     assert rel_err(y[:, rows], O.ref_gemv(x64, wd)) <= TOL_F32
+
+
+@pytest.mark.parametrize("qt", WTYPES, ids=[O.QNAMES[q] for q in WTYPES])
+def test_gemm_q_fp16_wide_tiles(dev, qt):
+    """M >= 256 takes 256-row tiles (512 threads, weight tile decoded once per
+    256 rows); M < 256 the 128-row tiles.  Both multiply the same fp16 operand
+    values in the same MFMA order, so the first 255 rows of an M = 300 product
+    equal the M = 255 product bit for bit; both match the oracle."""
+    import torch
+    from vkflame_amd import ops
+    N, K = 333, 1024
+    w = O.gen_weight(qt, N, K, seed_for(3, 90 + qt))
+    x = _f16(np.random.default_rng(seed_for(3, 100 + qt)), 300, K)
+    wd, xd = to_dev(w, dev), to_dev(x, dev)
+    y_wide = ops.gemm_q(wd, qt, xd, N, K).cpu().numpy()
+    y_narrow = ops.gemm_q(wd, qt, xd[:255], N, K).cpu().numpy()
+    torch.cuda.synchronize()
+    assert bits_equal(y_wide[:255], y_narrow), first_mismatch(y_wide[:255], y_narrow)
+    ref = O.ref_gemv(x.astype(np.float64), O.np_dequant(qt, w).reshape(N, K))
+    assert rel_err(y_wide, ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("qt,M,K", [(O.Q4_0, 200, 1024), (O.Q4_0, 64, 96), (O.Q4_K, 300, 1024), (O.Q8_0, 200, 512),
+                                    (O.Q6_K, 300, 2048), (O.Q5_K, 256, 768)],
+                         ids=["q4_0", "q4_0-k96", "q4_k-m300", "q8_0", "q6_k-m300", "q5_k-m256"])
+def test_gemm_q_q8_1_workspace_paths(dev, qt, M, K):
+    """Q8_1 activations at M > 16 take three routes: decoded once into a
+    caller workspace (vkflame_dispatch_gemm_q_ws, then the fp16-activation
+    GEMM), into a stream-ordered allocation of the library's
+    (vkflame_dispatch_gemm_q), or per tile inside the Q8_1 GEMM (no
+    workspace).  Every route multiplies the same fp16 operand values in the
+    same MFMA order: the two workspace routes agree bit for bit, the per-tile
+    route too where all take the direct-to-LDS main loops (K % 64 == 0), and
+    all match the oracle."""
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd import _lib as L
+    N = 300
+    w = O.gen_weight(qt, N, K, seed_for(3, 70 + qt))
+    x = np.random.default_rng(seed_for(3, 80 + qt)).normal(0, 1, (M, K)).astype(np.float32)
+    xq = O.np_quantize_q8_1(x).reshape(M, -1)
+    wd, xd = to_dev(w, dev), to_dev(xq, dev)
+    assert L.lib().vkflame_gemm_q_workspace_bytes(L.DTYPE_Q8_1, M, K) == M * K * 2
+    assert L.lib().vkflame_gemm_q_workspace_bytes(L.DTYPE_Q8_1, 16, K) == 0
+    assert L.lib().vkflame_gemm_q_workspace_bytes(L.DTYPE_FP16, M, K) == 0
+    y_ws = ops.gemm_q(wd, qt, xd, N, K)
+    y_tile = ops.gemm_q(wd, qt, xd, N, K, workspace=False)
+    y_lib = torch.empty((M, N), dtype=torch.float32, device=dev)
+    L.check(L.lib().vkflame_dispatch_gemm_q(ops._p(wd), qt, 0, ops._p(xd), L.DTYPE_Q8_1, xd.stride(0),
+                                            ops._p(y_lib), N, M, N, K, ops._stream()), "gemm_q")
+    torch.cuda.synchronize()
+    a, b, c = y_ws.cpu().numpy(), y_tile.cpu().numpy(), y_lib.cpu().numpy()
+    assert bits_equal(a, c), first_mismatch(a, c)
+    if K % 64 == 0:
+        assert bits_equal(a, b), first_mismatch(a, b)
+    x64 = O.np_dequant(O.Q8_1, xq).reshape(M, K).astype(np.float64)
+    ref = O.ref_gemv(x64, O.np_dequant(qt, w).reshape(N, K))
+    for y in (a, b, c):
+        assert rel_err(y, ref) <= TOL_F32

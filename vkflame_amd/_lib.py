@@ -55,6 +55,9 @@ def lib() -> ctypes.CDLL:
     L.vkflame_dispatch_dequant.argtypes = [P, P, U64, I, I, P]
     L.vkflame_quantize_q8_1.argtypes = [P, P, I, I, I64, P]
     L.vkflame_dispatch_gemm_q.argtypes = [P, I, U64, P, I, I64, P, I64, I, I, I, P]
+    L.vkflame_dispatch_gemm_q_ws.argtypes = [P, I, U64, P, I, I64, P, I64, I, I, I, P, ctypes.c_size_t, P]
+    L.vkflame_gemm_q_workspace_bytes.argtypes = [I, I, I]
+    L.vkflame_gemm_q_workspace_bytes.restype = ctypes.c_size_t
     L.vkflame_q6_k_q8_1_partials.argtypes = [P, P, P, I, I, I, P]
     L.vkflame_dispatch_linear.argtypes = [P, P, P, P, I, I, I, I, I, I, I, P, P, P]
     L.vkflame_dispatch_linear_int8.argtypes = [P, P, P, P, P, I, P, I, I, I, I, I, P]
@@ -63,6 +66,7 @@ def lib() -> ctypes.CDLL:
                                          ctypes.POINTER(P), ctypes.POINTER(LaunchPlan)]
     L.vkflame_execute_launch.argtypes = [ctypes.POINTER(LaunchPlan), P]
     for f in ("vkflame_dispatch_dequant", "vkflame_quantize_q8_1", "vkflame_dispatch_gemm_q",
+              "vkflame_dispatch_gemm_q_ws",
               "vkflame_q6_k_q8_1_partials", "vkflame_dispatch_linear", "vkflame_dispatch_linear_int8",
               "vkflame_resolve_launch", "vkflame_execute_launch", "vkflame_init",
               "vkflame_block_bytes", "vkflame_block_elems"):

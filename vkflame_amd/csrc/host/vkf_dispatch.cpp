@@ -134,8 +134,31 @@ int vkflame_quantize_q8_1(const float *x, void *dst, int M, int K, int64_t ldx, 
     return vkf::launch(VKF_K_QUANT_Q8_1, dim3(cdiv((uint64_t)M * K, 256)), dim3(256), a, S(stream));
 }
 
+size_t vkflame_gemm_q_workspace_bytes(int x_dtype, int M, int K) {
+    // fp16 copy of Q8_1 activations for the prefill GEMM
+    if (x_dtype != VKF_DTYPE_Q8_1 || M <= 16 || K <= 0 || (K % 32) != 0) return 0;
+    return (size_t)M * (size_t)K * 2;
+}
+
 int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const void *x, int x_dtype, int64_t ldx,
                             float *y, int64_t ldy, int M, int N, int K, void *stream) {
+    const size_t ws = vkflame_gemm_q_workspace_bytes(x_dtype, M, K);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (ws == 0 || N <= 0 || hipStreamIsCapturing(S(stream), &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+        return vkflame_dispatch_gemm_q_ws(w, qt, row_bytes, x, x_dtype, ldx, y, ldy, M, N, K, nullptr, 0, stream);
+    void *buf = nullptr;
+    if (hipMallocAsync(&buf, ws, S(stream)) != hipSuccess) {
+        (void)hipGetLastError();
+        return vkflame_dispatch_gemm_q_ws(w, qt, row_bytes, x, x_dtype, ldx, y, ldy, M, N, K, nullptr, 0, stream);
+    }
+    const int rc = vkflame_dispatch_gemm_q_ws(w, qt, row_bytes, x, x_dtype, ldx, y, ldy, M, N, K, buf, ws, stream);
+    const int rf = hipFreeAsync(buf, S(stream));
+    return rc ? rc : rf;
+}
+
+int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const void *x, int x_dtype, int64_t ldx,
+                               float *y, int64_t ldy, int M, int N, int K, void *workspace, size_t workspace_bytes,
+                               void *stream) {
     if (qt < 0 || qt > 6) return kInval;  // Q8_1 is an activation format, not a weight format
     if (M < 0 || N < 0 || K < 0 || (K % kBlockElems[qt]) != 0) return kInval;
     if (M == 0 || N == 0) return kOk;
@@ -236,6 +259,17 @@ int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const voi
         return vkf::launch(gemv_kernel(qt, xk), dim3(cdiv(N, 4)), dim3(256), a, S(stream));
     }
     if (xk == 1) return kNotSup;  // prefill takes fp16 or Q8_1 activations
+    if (xk == 2 && workspace && workspace_bytes >= vkflame_gemm_q_workspace_bytes(x_dtype, M, K) &&
+        aligned(workspace, 16) && ldx == (int64_t)(K / 32) * 36) {
+        // decode the activations once (fp16(d*q), the value the Q8_1 GEMM's
+        // own tile decode produces) and run the fp16-activation GEMM
+        const int rc = vkflame_dispatch_dequant(x, workspace, (uint64_t)M * (uint64_t)(K / 32), VKF_Q8_1,
+                                                VKF_DTYPE_FP16, stream);
+        if (rc) return rc;
+        x = workspace;
+        xk = 0;
+        ldx = K;
+    }
     VkfGemmArgs g{};
     g.X = x;
     g.Y = w;
@@ -249,6 +283,15 @@ int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const voi
     g.alpha = 1.0f;
     g.beta = 0.0f;
     g.flags = VKF_GF_D_F32;
+    // Wide 256 x 128 tiles (kernels/gemm.hip gemm_mainloop_wide) from
+    // M = 256 with fp16 activations that suit its direct-to-LDS loads
+    // (16-byte aligned rows, K % 64 == 0): each weight tile decoded once per
+    // 256 activation rows.
+    if (M >= 256 && xk == 0 && aligned(x, 16) && (ldx % 8) == 0 && (K % 64) == 0) {
+        const int fi = (gemm_kernel(qt, 0) - VKF_K_GEMM_Q4_0_F16) / 2;
+        return vkf::launch((VkfKernelId)(VKF_K_GEMM_W_Q4_0_F16 + fi), dim3(cdiv(N, 128), cdiv(M, 256)), dim3(512), g,
+                           S(stream));
+    }
     dim3 grid(cdiv(N, 128), cdiv(M, 128));
     return vkf::launch(gemm_kernel(qt, xk), grid, dim3(256), g, S(stream));
 }

@@ -96,7 +96,15 @@
     X(GEMM_Q5_K_F16, "vkf_gemm_q5_k_f16")                   \
     X(GEMM_Q5_K_Q81, "vkf_gemm_q5_k_q8_1")                  \
     X(GEMM_Q6_K_F16, "vkf_gemm_q6_k_f16")                   \
-    X(GEMM_Q6_K_Q81, "vkf_gemm_q6_k_q8_1")
+    X(GEMM_Q6_K_Q81, "vkf_gemm_q6_k_q8_1")                  \
+    /* wide (256 x 128 tile, 512 threads) GEMM, fp16 activations */ \
+    X(GEMM_W_Q4_0_F16, "vkf_gemm_q4_0_f16_w")               \
+    X(GEMM_W_Q4_1_F16, "vkf_gemm_q4_1_f16_w")               \
+    X(GEMM_W_Q8_0_F16, "vkf_gemm_q8_0_f16_w")               \
+    X(GEMM_W_Q5_0_F16, "vkf_gemm_q5_0_f16_w")               \
+    X(GEMM_W_Q4_K_F16, "vkf_gemm_q4_k_f16_w")               \
+    X(GEMM_W_Q5_K_F16, "vkf_gemm_q5_k_f16_w")               \
+    X(GEMM_W_Q6_K_F16, "vkf_gemm_q6_k_f16_w")
 
 enum VkfKernelId {
 #define VKF_X(id, sym) VKF_K_##id,

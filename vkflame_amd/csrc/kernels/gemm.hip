@@ -697,13 +697,13 @@ __device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_
 // (pitch 132 floats) and written out as 16-byte row vectors when D's rows
 // allow it, element by element otherwise.  smem must be free (the main loop
 // ends with a barrier).
+// epi_stage: one wave's 64x64 values (position wr, wc inside the 128x128
+// tile at r0, c0) finished and written to the fp32 staging tile.
 template <class ACC>
-__device__ __forceinline__ void epilogue_tile(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC acc[4][4],
-                                              uint8_t *smem) {
+__device__ __forceinline__ void epi_stage(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC acc[4][4],
+                                          float *tile, int wr, int wc) {
     constexpr int TP = 132;
-    const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
     const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
-    float *tile = (float *)smem;
     float csv[4], bcv[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -740,12 +740,17 @@ __device__ __forceinline__ void epilogue_tile(const VkfGemmArgs &a, uint32_t r0,
                 tile[tr * TP + wc * 64 + 16 * j + li] = vkf_act(a.act, v);
             }
         }
-    __syncthreads();
+}
+
+// epi_store: the staged 128x128 tile to D by all NT threads of the workgroup.
+template <int NT>
+__device__ __forceinline__ void epi_store(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const float *tile) {
+    constexpr int TP = 132;
     const bool f32 = (a.flags & VKF_GF_D_F32) != 0;
     const uint32_t vec = f32 ? 4 : 8;  // elements per 16-byte store
     const bool vok = (a.ldd % vec) == 0 && (((uintptr_t)a.D & 15) == 0);
     const uint32_t per_row = 128 / vec;
-    for (uint32_t q = threadIdx.x; q < 128 * per_row; q += 256) {
+    for (uint32_t q = threadIdx.x; q < 128 * per_row; q += NT) {
         const uint32_t tr = q / per_row, tc = (q % per_row) * vec;
         const uint32_t r = r0 + tr, c = c0 + tc;
         if (r >= a.R || c >= a.Cn) continue;
@@ -768,6 +773,15 @@ __device__ __forceinline__ void epilogue_tile(const VkfGemmArgs &a, uint32_t r0,
     }
 }
 
+template <class ACC>
+__device__ __forceinline__ void epilogue_tile(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC acc[4][4],
+                                              uint8_t *smem) {
+    const int wave = threadIdx.x >> 6;
+    epi_stage(a, r0, c0, acc, (float *)smem, wave >> 1, wave & 1);
+    __syncthreads();
+    epi_store<256>(a, r0, c0, (const float *)smem);
+}
+
 // Workgroup -> 128 x 128 tile, XCD-aware.  Workgroups are dispatched to the
 // 8 XCDs round-robin (id % 8), each XCD with its own L2.  Columns (Y tiles)
 // are dealt to XCDs round-robin and an XCD runs all row tiles of a column
@@ -775,6 +789,7 @@ __device__ __forceinline__ void epilogue_tile(const VkfGemmArgs &a, uint32_t r0,
 // row tile (for the vocabulary projection, 512 x 152064 x 5120, that is 4x
 // fewer weight bytes from HBM than a row-major order).  Columns past the
 // last multiple of 8 go in plain order.
+template <uint32_t RT = 128>
 __device__ __forceinline__ void gemm_tile_of(uint32_t &r0, uint32_t &c0) {
     const uint32_t nc = gridDim.x, nr = gridDim.y, id = blockIdx.x + nc * blockIdx.y;
     const uint32_t full = nc & ~7u;
@@ -788,7 +803,7 @@ __device__ __forceinline__ void gemm_tile_of(uint32_t &r0, uint32_t &c0) {
         c = full + j / nr;
         r = j % nr;
     }
-    r0 = r * 128;
+    r0 = r * RT;
     c0 = c * 128;
 }
 
@@ -852,6 +867,107 @@ VKF_GEMM_Q_Q81(q5_0, VKF_Q5_0)
 VKF_GEMM_Q_Q81(q4_k, VKF_Q4_K)
 VKF_GEMM_Q_Q81(q5_k, VKF_Q5_K)
 VKF_GEMM_Q_Q81(q6_k, VKF_Q6_K)
+
+// ---------------------------------------------------------------------------
+// Wide quantised-weight GEMM with fp16 activations: 512 threads, a 256 x 128
+// tile (activation rows x weight rows), eight waves of 64 x 64 (wave w: rows
+// 64*(w/2), columns 64*(w%2)).  Against two 128 x 128 workgroups, each weight
+// tile is loaded and decoded once per 256 activation rows instead of once
+// per 128, which halves the decode work per MAC; the decode's VALU time is
+// what bounds these GEMMs (Q6_K 512 x 152064 x 5120 on MI355X: 1.56 ms here
+// against 1.75 ms with 128 x 128 tiles).  Waves 0-3 decode the weight tile
+// (QStage, thread t: row t/2, chunk t&1); the activation tile comes by
+// direct-to-LDS loads from all eight waves.  Two stages of 48 KiB (32 KiB
+// activations + 16 KiB weights); the epilogue's 256-row fp32 staging tile
+// (132 KiB) sets the LDS size.
+// ---------------------------------------------------------------------------
+#define GEMM_W_STAGE 49152
+#define GEMM_W_LDS (2 * GEMM_W_STAGE)
+#define GEMM_KERNEL_W VKF_KERNEL void __launch_bounds__(512)
+
+template <int QT>
+__device__ __forceinline__ void gemm_mainloop_wide(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, vkf_f4 acc[4][4],
+                                                   uint8_t *smem) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wr = wave >> 1, wc = wave & 1;
+    const bool ywave = threadIdx.x < 256;  // wave-uniform
+    const uint32_t nk = a.K / 64;
+    const uint8_t *gx[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t rr = (4 * wave + j) * 8 + (lane >> 3);  // 0..255
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t rx = r0 + rr < a.R ? r0 + rr : a.R - 1;
+        gx[j] = (const uint8_t *)a.X + (uint64_t)rx * a.ldx * 2 + ch * 16;
+    }
+    auto issue_x = [&](uint32_t kt, uint32_t stage) {
+        uint8_t *sx = smem + stage * GEMM_W_STAGE;
+#pragma unroll
+        for (int j = 0; j < 4; j++) vkf_load_lds16(gx[j] + (uint64_t)kt * 128, sx + (4 * wave + j) * 1024);
+    };
+    const uint32_t yr = threadIdx.x >> 1, yh = threadIdx.x & 1;
+    auto store_y = [&](uint32_t stage, const TileRegs &t) {
+        uint8_t *sy = smem + stage * GEMM_W_STAGE + 32768 + yr * 128;
+#pragma unroll
+        for (int g = 0; g < 4; g++) *(vkf_i4 *)(sy + (((4 * yh + g) ^ (yr & 7)) << 4)) = t.v[g];
+    };
+    QStage<QT> q;
+    TileRegs ty;
+    issue_x(0, 0);
+    if (ywave) {
+        q.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, 0);
+        q.decode(ty);
+        store_y(0, ty);
+    }
+    wait_vm<0>();
+    __syncthreads();
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        const uint32_t cur = kt & 1;
+        if (kt + 1 < nk) {
+            issue_x(kt + 1, cur ^ 1);
+            if (ywave) q.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, (kt + 1) * 64);
+        }
+        const uint8_t *lx = smem + cur * GEMM_W_STAGE;
+        mfma_step_swz<2>(lx, lx + 32768, wr, wc, acc);
+        if (kt + 1 < nk && ywave) {
+            q.decode(ty);
+            store_y(cur ^ 1, ty);
+        }
+        wait_vm<0>();
+        __syncthreads();
+    }
+}
+
+template <int QT>
+__device__ __forceinline__ void gemm_wide_body(const VkfGemmArgs &a) {
+    uint32_t r0, c0;
+    gemm_tile_of<256>(r0, c0);
+    vkf_f4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_W_LDS > 256 * 132 * 4 ? GEMM_W_LDS : 256 * 132 * 4];
+    gemm_mainloop_wide<QT>(a, r0, c0, acc, smem);
+    // epilogue: both 128-row halves staged at once (256 x 132 fp32; staging
+    // them one after the other costs the kernel its registers)
+    const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
+    float *tile = (float *)smem + (wr >> 1) * 128 * 132;
+    epi_stage(a, r0 + 128 * (wr >> 1), c0, acc, tile, wr & 1, wc);
+    __syncthreads();
+    epi_store<512>(a, r0, c0, (const float *)smem);
+    epi_store<512>(a, r0 + 128, c0, (const float *)smem + 128 * 132);
+}
+
+// dense fp16 activations only: 16-byte aligned rows, K % 64 == 0
+#define VKF_GEMM_W(name, QT) \
+    GEMM_KERNEL_W vkf_gemm_##name##_f16_w(VkfGemmArgs a) { gemm_wide_body<QT>(a); }
+VKF_GEMM_W(q4_0, VKF_Q4_0)
+VKF_GEMM_W(q4_1, VKF_Q4_1)
+VKF_GEMM_W(q8_0, VKF_Q8_0)
+VKF_GEMM_W(q5_0, VKF_Q5_0)
+VKF_GEMM_W(q4_k, VKF_Q4_K)
+VKF_GEMM_W(q5_k, VKF_Q5_K)
+VKF_GEMM_W(q6_k, VKF_Q6_K)
 
 // ---------------------------------------------------------------------------
 // int8 x int8 -> int32 (kernels/linear_int8.glsl:54-93, with int8 A).

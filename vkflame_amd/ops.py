@@ -49,9 +49,11 @@ def quantize_q8_1(x: torch.Tensor) -> torch.Tensor:
 
 
 def gemm_q(w: torch.Tensor, qtype: int, x: torch.Tensor, N: int, K: int, M: int | None = None,
-           out: torch.Tensor | None = None) -> torch.Tensor:
+           out: torch.Tensor | None = None, workspace: bool = True) -> torch.Tensor:
     """y[M, N] fp32 = x[M, K] @ deq(w)[N, K]^T.  x: fp16 / fp32 [M, K] or
-    uint8 Q8_1 rows [M, K/32*36]."""
+    uint8 Q8_1 rows [M, K/32*36].  Q8_1 activations at M > 16 get a torch
+    workspace for their one-time fp16 decode (vkflame_dispatch_gemm_q_ws);
+    workspace=False makes the GEMM decode them per tile instead."""
     if x.dtype == torch.float16:
         xd, ldx = L.DTYPE_FP16, x.stride(0)
     elif x.dtype == torch.float32:
@@ -63,8 +65,10 @@ def gemm_q(w: torch.Tensor, qtype: int, x: torch.Tensor, N: int, K: int, M: int 
     M = x.shape[0] if M is None else M
     y = torch.empty((M, N), dtype=torch.float32, device=x.device) if out is None else out
     row_bytes = w.stride(0) if w.dim() == 2 else 0
-    check(lib().vkflame_dispatch_gemm_q(_p(w), qtype, row_bytes, _p(x), xd, ldx, _p(y), y.stride(0), M, N, K,
-                                        _stream()), "gemm_q")
+    nws = lib().vkflame_gemm_q_workspace_bytes(xd, M, K) if workspace else 0
+    ws = torch.empty(nws, dtype=torch.uint8, device=x.device) if nws else None
+    check(lib().vkflame_dispatch_gemm_q_ws(_p(w), qtype, row_bytes, _p(x), xd, ldx, _p(y), y.stride(0), M, N, K,
+                                           _p(ws), nws, _stream()), "gemm_q")
     return y
 
 
