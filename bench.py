@@ -279,7 +279,7 @@ def main():
             traffic = json.load(f).get("hbm_bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "vkf_gemv_dot_q4_k_f16_m1", "algorithmic_bytes_per_launch": alg_bytes}
+                "kernel": "vkf_gemv_dotl_q4_k_f16", "algorithmic_bytes_per_launch": alg_bytes}
 
     suite = None if args.no_suite else run_suite(torch, ops, O, reps=20)
     cpu = None if args.no_cpu else cpu_baseline(O, N, K, wbytes, seed)
