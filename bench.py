@@ -266,6 +266,13 @@ def main():
     err = O.max_rel_err(y.cpu().numpy()[:, rows], ref)
     log(f"primary: {ms * 1e3:.2f} us/launch over {steps} launches, {len(copies)} rotating copies, "
         f"max rel err {err:.2e}")
+    # measured read-bandwidth reference: a plain coalesced read of the same
+    # weight copies, timed the same way (library kernel vkf_stream_read)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    s_launches = [(lambda c=copies[i % len(copies)]: ops.stream_read(c, sink)) for i in range(steps)]
+    ms_stream = r.time_graph(s_launches, reps=1, warmup=max(1, args.warmup // max(1, steps)))
+    stream_gbs = wbytes / (ms_stream * 1e-3) / 1e9
+    log(f"stream read of the same {wbytes} B: {ms_stream * 1e3:.2f} us/launch, {stream_gbs:.0f} GB/s")
     del copies
     torch.cuda.empty_cache()
 
@@ -279,7 +286,8 @@ def main():
             traffic = json.load(f).get("hbm_bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "vkf_gemv_dotl_q4_k_f16", "algorithmic_bytes_per_launch": alg_bytes}
+                "kernel": "vkf_gemv_dotl_q4_k_f16", "algorithmic_bytes_per_launch": alg_bytes,
+                "stream_read_GBps": round(stream_gbs, 1), "frac_of_stream_read": round(value / stream_gbs, 4)}
 
     suite = None if args.no_suite else run_suite(torch, ops, O, reps=20)
     cpu = None if args.no_cpu else cpu_baseline(O, N, K, wbytes, seed)

@@ -124,6 +124,14 @@ size_t vkflame_gemm_q_workspace_bytes(int x_dtype, int M, int K);
  * Q6_K x Q8_1 product. */
 int vkflame_q6_k_q8_1_partials(const void *w, const void *xq, int32_t *P, int M, int N, int K, void *stream);
 
+/* Measurement hook: reads bytes (a multiple of 16) from src (16-byte
+ * aligned) once with coalesced 16-byte loads and nothing else; sink is a
+ * device word that is written only if the folded data equals a constant.
+ * Its duration is the measured HBM read-bandwidth reference for the decode
+ * GEMVs' weight streams.  No reference counterpart (the reference has no
+ * bandwidth probe). */
+int vkflame_stream_read(const void *src, uint64_t bytes, uint32_t *sink, void *stream);
+
 /* Row-major linear layer, the reference's vkflame_dispatch_linear
  * (runtime/dispatch.h:51-58, runtime/dispatch.cpp:253-326) with the arguments
  * it ignores honoured:

@@ -161,6 +161,17 @@ def test_c_abi_rejects_bad_arguments():
     assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 2, 0, 1, 1, None, None, s) == 1
     assert L.vkflame_dispatch_linear_int8(P(16), None, P(16), None, None, 1, P(16), 2, 4, 4, 4, 0, s) == 1
     assert L.vkflame_q6_k_q8_1_partials(P(16), P(16), P(16), 1, 1, 100, s) == 1
+    assert L.vkflame_stream_read(P(16), 17, P(16), s) == 1                    # bytes % 16
+    assert L.vkflame_stream_read(P(8), 32, P(16), s) == 1                     # src not 16-aligned
+    assert L.vkflame_stream_read(P(16), 32, None, s) == 1                     # no sink
+    assert L.vkflame_stream_read(None, 0, None, s) == 0                       # empty: no-op
+    ws = L.vkflame_gemm_q_workspace_bytes
+    assert ws(VL.DTYPE_Q8_1, 512, 5120) == 512 * 5120 * 2
+    assert ws(VL.DTYPE_Q8_1, 16, 5120) == 0 and ws(VL.DTYPE_FP16, 512, 5120) == 0 and ws(VL.DTYPE_Q8_1, 64, 100) == 0
+    qws = L.vkflame_dispatch_gemm_q_ws
+    assert qws(P(16), 4, 0, P(16), 1, 0, P(16), 0, 1, 8, 300, None, 0, s) == 1     # K % 256
+    assert qws(P(16), 6, 0, P(18), 11, 0, P(16), 0, 64, 8, 256, P(16), 1 << 20, s) == 1  # Q8_1 x not 4-aligned
+    assert qws(P(16), 6, 0, P(16), 11, 0, P(16), 0, 0, 8, 256, P(16), 1 << 20, s) == 0   # M = 0: no-op
     assert L.vkflame_execute_launch(ctypes.byref(VL.LaunchPlan()), s) == 1
 
 

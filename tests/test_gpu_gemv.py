@@ -239,3 +239,16 @@ def test_gemv_dot_lds_tails(dev, qt, kind, NK):
     y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
     rows = np.unique(np.concatenate([np.arange(0, N, max(1, N // 150)), [N - 1]]))
     assert _rows_check(y, x64, w, qt, K, rows) <= TOL_F32
+
+
+def test_stream_read_hook(dev):
+    """The read-bandwidth hook reads a buffer (ragged last pass included) and
+    leaves the sink alone unless the folded data hits its constant."""
+    import torch
+    from vkflame_amd import ops
+    sink = torch.full((1,), 7, dtype=torch.int32, device=dev)
+    for nbytes in (16, 4096 + 16, 39813120):
+        buf = torch.arange(nbytes // 4, dtype=torch.int32, device=dev)
+        ops.stream_read(buf, sink)
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 7

@@ -125,6 +125,14 @@ int vkflame_dispatch_dequant(const void *src, void *dst, uint64_t n_blocks, int 
     return vkf::launch(k, dim3(cdiv(threads, 256)), dim3(256), a, S(stream));
 }
 
+int vkflame_stream_read(const void *src, uint64_t bytes, uint32_t *sink, void *stream) {
+    if ((bytes % 16) != 0) return kInval;
+    if (bytes == 0) return kOk;
+    if (!src || !sink || !aligned(src, 16) || !aligned(sink, 4)) return kInval;
+    VkfStreamArgs a{src, sink, bytes / 16};
+    return vkf::launch(VKF_K_STREAM_READ, dim3(4 * vkf::cu_count()), dim3(256), a, S(stream));
+}
+
 int vkflame_quantize_q8_1(const float *x, void *dst, int M, int K, int64_t ldx, void *stream) {
     if (M < 0 || K < 0 || (K % 32) != 0) return kInval;
     if (M == 0 || K == 0) return kOk;

@@ -42,6 +42,13 @@ struct VkfQuantizeArgs {
     uint32_t M, K;
 };
 
+// Read-bandwidth measurement: n16 16-byte vectors read once from src.
+struct VkfStreamArgs {
+    const void *src;
+    uint32_t *sink;
+    uint64_t n16;
+};
+
 // Decode GEMV / small GEMM: y[m, n] = sum_k x[m, k] * W[n, k], M <= 16.
 // W row n starts at w + n*row_bytes.  x is fp16 or fp32 (by kernel), or Q8_1
 // blocks (row m at x + m*ldx bytes) for the Q6_K x Q8_1 kernel.
@@ -95,6 +102,7 @@ struct VkfGemmArgs {
 #ifdef __cplusplus
 static_assert(sizeof(VkfDequantArgs) == 24, "VkfDequantArgs layout");
 static_assert(sizeof(VkfQuantizeArgs) == 32, "VkfQuantizeArgs layout");
+static_assert(sizeof(VkfStreamArgs) == 24, "VkfStreamArgs layout");
 static_assert(sizeof(VkfGemvArgs) == 64, "VkfGemvArgs layout");
 static_assert(sizeof(VkfGemmArgs) == 120, "VkfGemmArgs layout");
 #endif

@@ -78,6 +78,12 @@ def q6k_q81_partials(w: torch.Tensor, xq: torch.Tensor, M: int, N: int, K: int) 
     return P
 
 
+def stream_read(src: torch.Tensor, sink: torch.Tensor) -> None:
+    """Read all of src once (the HBM read-bandwidth reference); sink: a
+    device int32 tensor the kernel may write one word of."""
+    check(lib().vkflame_stream_read(_p(src), src.numel() * src.element_size(), _p(sink), _stream()), "stream_read")
+
+
 def linear(A, B, M, N, K, dtype_code, transA=0, transB=1, act=0, C=None, alpha=None, beta=None, out=None):
     """vkflame_dispatch_linear (row-major D[M,N] = act(alpha op(A) op(B) + beta C))."""
     if out is None:
