@@ -84,6 +84,16 @@ int vkflame_dispatch_dequant(const void *src, void *dst, uint64_t n_blocks, int 
  * but has no quantizer. */
 int vkflame_quantize_q8_1(const float *x, void *dst, int M, int K, int64_t ldx, void *stream);
 
+/* Symmetric per-row int8 quantisation of x[M, K] (x_dtype VKF_DTYPE_FP16 or
+ * VKF_DTYPE_FP32, row stride ldx elements, 0 = K): scale[m] = max(max_k
+ * |x[m,k]| / 127, 1e-8), q[m, k] = clamp(round_half_even(x[m,k] / scale[m]),
+ * -127, 127), q packed [M, K].  The rule of the reference's per-output-channel
+ * weight quantiser (tools/quantise.py:35-41), used here also per token for the
+ * activations of the int8 linear (vkflame_dispatch_linear_int8's A and
+ * a_scale). */
+int vkflame_quantize_rows_i8(const void *x, int x_dtype, int M, int K, int64_t ldx, int8_t *q, float *scale,
+                             void *stream);
+
 /* y[M, N] (fp32, row stride ldy) = x[M, K] @ Wdeq[N, K]^T.
  * w: N rows of K/block_elems blocks of quant_type, row stride row_bytes
  *    (0 = packed: K/block_elems*block_bytes).

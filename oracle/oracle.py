@@ -59,6 +59,8 @@ class _C:
             lib.vkfo_dequant_f16.argtypes = [ctypes.c_int, P, ctypes.c_size_t, P]
             lib.vkfo_quantize_q8_1.argtypes = [P, ctypes.c_size_t, P]
             lib.vkfo_quantize_q8_1.restype = None
+            lib.vkfo_quantize_rows_i8.argtypes = [P, ctypes.c_int, ctypes.c_int, P, P]
+            lib.vkfo_quantize_rows_i8.restype = None
             lib.vkfo_gemm_i8_nt.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
             lib.vkfo_q6k_q8_1_partials.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
             lib.vkfo_q6k_q8_1_partials.restype = None
@@ -103,6 +105,16 @@ def c_quantize_q8_1(x: np.ndarray) -> np.ndarray:
     out = np.empty(x.size // 32 * 36, dtype=np.uint8)
     _C.lib().vkfo_quantize_q8_1(_ptr(x), x.size, _ptr(out))
     return out
+
+
+def c_quantize_rows_i8(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Per-row symmetric int8 quantiser (tools/quantise.py:35-41 rule)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    q = np.empty((M, K), dtype=np.int8)
+    scale = np.empty(M, dtype=np.float32)
+    _C.lib().vkfo_quantize_rows_i8(_ptr(x), M, K, _ptr(q), _ptr(scale))
+    return q, scale
 
 
 def c_gemm_i8_nt(A: np.ndarray, B: np.ndarray) -> np.ndarray:
@@ -240,6 +252,17 @@ def np_quantize_q8_1(x: np.ndarray) -> np.ndarray:
         out[:, 2:4] = s.astype(np.float16).view(np.uint8).reshape(-1, 2)
     out[:, 4:36] = q.astype(np.int8).view(np.uint8)
     return out.reshape(-1)
+
+
+def np_quantize_rows_i8(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Vectorised twin of c_quantize_rows_i8: the reference's per-output-channel
+    weight quantiser (tools/quantise.py:35-41) -- scale = max|row|/127 clamped
+    to >= 1e-8, q = round(x/scale) (half to even, as torch.round) clamped to
+    +-127 -- applied to each row (weights per channel, activations per token)."""
+    x = np.ascontiguousarray(x, dtype=F32)
+    scale = np.maximum((np.abs(x).max(axis=1) / F32(127.0)).astype(F32), F32(1e-8))
+    q = np.clip(np.rint((x / scale[:, None]).astype(F32)), -127, 127).astype(np.int8)
+    return q, scale
 
 
 def np_act(act: int, x: np.ndarray) -> np.ndarray:

@@ -298,6 +298,33 @@ int vkfo_dequant_f16(int qtype, const uint8_t *src, size_t n_blocks, uint16_t *d
 }
 
 /* ------------------------------------------------------------------ */
+/* Symmetric per-row int8 quantiser, the rule of the reference's weight */
+/* quantiser (tools/quantise.py:35-41): scale = max|row|/127 clamped to */
+/* >= 1e-8, q = round-half-even(x/scale) clamped to +-127.              */
+/* ------------------------------------------------------------------ */
+
+void vkfo_quantize_rows_i8(const float *x, int M, int K, int8_t *q, float *scale)
+{
+    for (int m = 0; m < M; m++) {
+        const float *xr = x + (size_t)m * K;
+        float amax = 0.0f;
+        for (int k = 0; k < K; k++) {
+            float a = fabsf(xr[k]);
+            amax = amax > a ? amax : a;
+        }
+        float s = amax / 127.0f;
+        if (s < 1e-8f) s = 1e-8f;
+        scale[m] = s;
+        for (int k = 0; k < K; k++) {
+            float v = rintf(xr[k] / s);
+            if (v > 127.0f) v = 127.0f;
+            if (v < -127.0f) v = -127.0f;
+            q[(size_t)m * K + k] = (int8_t)v;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
 /* Q8_1 quantizer (ggml quantize_row_q8_1_ref)                         */
 /* ------------------------------------------------------------------ */
 

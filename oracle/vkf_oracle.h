@@ -49,6 +49,7 @@ int vkfo_dequant_f16(int qtype, const uint8_t *src, size_t n_blocks, uint16_t *d
  * Follows ggml's reference quantizer quantize_row_q8_1_ref (ggml is not
  * vendored in the reference; kernels/dequant_q8_1.glsl:2-4 names the format). */
 void vkfo_quantize_q8_1(const float *x, size_t n, uint8_t *dst);
+void vkfo_quantize_rows_i8(const float *x, int M, int K, int8_t *q, float *scale);
 
 /* Integer GEMM, both operands K-contiguous: C[m,n] = sum_k A[m,k]*B[n,k].
  * Accumulates in int64; returns -1 if any result leaves int32 range. */

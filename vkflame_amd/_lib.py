@@ -60,6 +60,7 @@ def lib() -> ctypes.CDLL:
     L.vkflame_gemm_q_workspace_bytes.restype = ctypes.c_size_t
     L.vkflame_q6_k_q8_1_partials.argtypes = [P, P, P, I, I, I, P]
     L.vkflame_stream_read.argtypes = [P, U64, P, P]
+    L.vkflame_quantize_rows_i8.argtypes = [P, I, I, I, I64, P, P, P]
     L.vkflame_dispatch_linear.argtypes = [P, P, P, P, I, I, I, I, I, I, I, P, P, P]
     L.vkflame_dispatch_linear_int8.argtypes = [P, P, P, P, P, I, P, I, I, I, I, I, P]
     L.vkflame_resolve_launch.argtypes = [ctypes.c_char_p, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
@@ -69,7 +70,7 @@ def lib() -> ctypes.CDLL:
     for f in ("vkflame_dispatch_dequant", "vkflame_quantize_q8_1", "vkflame_dispatch_gemm_q",
               "vkflame_dispatch_gemm_q_ws",
               "vkflame_q6_k_q8_1_partials", "vkflame_dispatch_linear", "vkflame_dispatch_linear_int8",
-              "vkflame_stream_read",
+              "vkflame_stream_read", "vkflame_quantize_rows_i8",
               "vkflame_resolve_launch", "vkflame_execute_launch", "vkflame_init",
               "vkflame_block_bytes", "vkflame_block_elems"):
         getattr(L, f).restype = I

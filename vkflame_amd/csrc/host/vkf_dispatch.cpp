@@ -125,6 +125,17 @@ int vkflame_dispatch_dequant(const void *src, void *dst, uint64_t n_blocks, int 
     return vkf::launch(k, dim3(cdiv(threads, 256)), dim3(256), a, S(stream));
 }
 
+int vkflame_quantize_rows_i8(const void *x, int x_dtype, int M, int K, int64_t ldx, int8_t *q, float *scale,
+                             void *stream) {
+    if (M < 0 || K < 0 || (x_dtype != VKF_DTYPE_FP16 && x_dtype != VKF_DTYPE_FP32)) return kInval;
+    if (M == 0 || K == 0) return kOk;
+    if (ldx == 0) ldx = K;
+    const uintptr_t xa = x_dtype == VKF_DTYPE_FP16 ? 2 : 4;
+    if (!x || !q || !scale || ldx < K || !aligned(x, xa) || !aligned(scale, 4) || M > 0x7fffffff) return kInval;
+    VkfQuantRowsArgs a{x, q, scale, (uint64_t)ldx, (uint32_t)M, (uint32_t)K, x_dtype == VKF_DTYPE_FP16 ? 1u : 0u, 0u};
+    return vkf::launch(VKF_K_QUANT_ROWS_I8, dim3((uint32_t)M), dim3(256), a, S(stream));
+}
+
 int vkflame_stream_read(const void *src, uint64_t bytes, uint32_t *sink, void *stream) {
     if ((bytes % 16) != 0) return kInval;
     if (bytes == 0) return kOk;

@@ -31,6 +31,7 @@
     X(DEQ_Q8_1_F16, "vkf_dequant_q8_1_f16")                 \
     X(QUANT_Q8_1, "vkf_quantize_q8_1")                      \
     X(STREAM_READ, "vkf_stream_read")                       \
+    X(QUANT_ROWS_I8, "vkf_quantize_rows_i8")                \
     /* GEMV: 3 activation kinds per weight type, VKF_Q* order */ \
     X(GEMV_Q4_0_F16, "vkf_gemv_q4_0_f16")                   \
     X(GEMV_Q4_0_F32, "vkf_gemv_q4_0_f32")                   \

@@ -42,6 +42,18 @@ struct VkfQuantizeArgs {
     uint32_t M, K;
 };
 
+// Symmetric per-row int8 quantisation: scale[m] = max(max_k |x[m,k]| / 127,
+// 1e-8), q[m,k] = clamp(rint(x[m,k] / scale[m]), -127, 127).  x fp16 or fp32
+// (x_f16), row stride ldx elements; q packed [M, K].
+struct VkfQuantRowsArgs {
+    const void *x;
+    int8_t *q;
+    float *scale;
+    uint64_t ldx;
+    uint32_t M, K;
+    uint32_t x_f16, pad;
+};
+
 // Read-bandwidth measurement: n16 16-byte vectors read once from src.
 struct VkfStreamArgs {
     const void *src;
@@ -103,6 +115,7 @@ struct VkfGemmArgs {
 static_assert(sizeof(VkfDequantArgs) == 24, "VkfDequantArgs layout");
 static_assert(sizeof(VkfQuantizeArgs) == 32, "VkfQuantizeArgs layout");
 static_assert(sizeof(VkfStreamArgs) == 24, "VkfStreamArgs layout");
+static_assert(sizeof(VkfQuantRowsArgs) == 48, "VkfQuantRowsArgs layout");
 static_assert(sizeof(VkfGemvArgs) == 64, "VkfGemvArgs layout");
 static_assert(sizeof(VkfGemmArgs) == 120, "VkfGemmArgs layout");
 #endif

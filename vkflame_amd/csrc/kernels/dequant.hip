@@ -82,3 +82,35 @@ VKF_KERNEL void __launch_bounds__(256) vkf_quantize_q8_1(VkfQuantizeArgs a) {
         *(uint32_t *)blkp = hd | (hs << 16);
     }
 }
+
+// ---------------------------------------------------------------------------
+// Symmetric per-row int8 quantisation, the input step of the int8 linear:
+// the rule of the reference's weight quantiser (tools/quantise.py:35-41,
+// scale = max|row|/127 clamped to >= 1e-8, q = round(x/scale) clamped to
+// +-127, round half to even as torch.round) applied per output channel of a
+// weight or per token of an activation matrix.  One 256-thread workgroup per
+// row: a max reduction, then one rounding division per element (IEEE
+// correctly rounded, hipcc's default for fp32 divide), so the result is the
+// same bits as the sequential rule.
+// ---------------------------------------------------------------------------
+VKF_KERNEL void __launch_bounds__(256) vkf_quantize_rows_i8(VkfQuantRowsArgs a) {
+    __shared__ float red[4];
+    const uint64_t m = blockIdx.x;
+    const _Float16 *xh = (const _Float16 *)a.x + m * a.ldx;
+    const float *xf = (const float *)a.x + m * a.ldx;
+    auto ld = [&](uint32_t k) { return a.x_f16 ? (float)xh[k] : xf[k]; };
+    float amax = 0.0f;
+    for (uint32_t k = threadIdx.x; k < a.K; k += 256) amax = fmaxf(amax, fabsf(ld(k)));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float scale = fmaxf(amax / 127.0f, 1e-8f);
+    int8_t *q = a.q + m * a.K;
+    for (uint32_t k = threadIdx.x; k < a.K; k += 256) {
+        const float v = rintf(ld(k) / scale);
+        q[k] = (int8_t)(int)fminf(fmaxf(v, -127.0f), 127.0f);
+    }
+    if (threadIdx.x == 0) a.scale[m] = scale;
+}

@@ -78,6 +78,19 @@ def q6k_q81_partials(w: torch.Tensor, xq: torch.Tensor, M: int, N: int, K: int) 
     return P
 
 
+def quantize_rows_i8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp16 / fp32 [M, K] -> (int8 [M, K], fp32 scale [M]): symmetric per-row
+    quantisation (vkflame_quantize_rows_i8)."""
+    assert x.dim() == 2 and x.dtype in (torch.float16, torch.float32) and x.stride(1) == 1
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    scale = torch.empty(M, dtype=torch.float32, device=x.device)
+    xd = L.DTYPE_FP16 if x.dtype == torch.float16 else L.DTYPE_FP32
+    check(lib().vkflame_quantize_rows_i8(_p(x), xd, M, K, x.stride(0), _p(q), _p(scale), _stream()),
+          "quantize_rows_i8")
+    return q, scale
+
+
 def stream_read(src: torch.Tensor, sink: torch.Tensor) -> None:
     """Read all of src once (the HBM read-bandwidth reference); sink: a
     device int32 tensor the kernel may write one word of."""
