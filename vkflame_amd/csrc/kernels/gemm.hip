@@ -598,6 +598,101 @@ struct QStage<VKF_Q6_K> {
     }
 };
 
+// Half-chunk weight decoders for the 512-thread wide GEMM: thread t decodes
+// 16 elements -- row t/4 of the 128-row tile, elements 16*(t&3) .. +15 of
+// the 64-k step -- so that all eight waves share the decode.  Same values,
+// bit for bit, as the 32-element QStage decoders above.
+template <int QT>
+struct QHalf;
+
+// Q4_K: half h of sub-block j: qs bytes 16 + 32(j/2) + 16h .. +15, nibble j&1.
+template <>
+struct QHalf<VKF_Q4_K> {
+    vkf_u4 hdr, qs;
+    uint32_t j;
+    bool live;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        const uint32_t r = row0 + (threadIdx.x >> 2), kc = k0 + 32 * ((threadIdx.x >> 1) & 1);
+        const uint32_t h = threadIdx.x & 1;
+        live = r < nrows && kc < K;
+        const uint32_t rr = r < nrows ? r : nrows - 1, kk = kc < K ? kc : 0;
+        const uint8_t *blk = W + (uint64_t)rr * row_bytes + 144ull * (kk / 256);
+        j = (kk % 256) / 32;
+        hdr = *(const vkf_u4 *)blk;
+        qs = *(const vkf_u4 *)(blk + 16 + 32 * (j >> 1) + 16 * h);
+    }
+    __device__ __forceinline__ void decode(vkf_i4 out[2]) {
+        const float dall = vkf_h2f(hdr[0] & 0xffffu), dmin = vkf_h2f(hdr[0] >> 16);
+        const uint32_t s0 = hdr[1], s4 = hdr[2], s8 = hdr[3];
+        const uint32_t scW = j < 4 ? (s0 & 0x3f3f3f3fu) : ((s8 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u));
+        const uint32_t mnW = j < 4 ? (s4 & 0x3f3f3f3fu) : (((s8 >> 4) & 0x0f0f0f0fu) | ((s4 >> 2) & 0x30303030u));
+        const uint32_t sh = 8 * (j & 3);
+        const float dsc = dall * (float)((scW >> sh) & 0xffu), dm = dmin * (float)((mnW >> sh) & 0xffu);
+        const uint32_t nsh = 4 * (j & 1);
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            vkf_h8 v;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t n = (qs[2 * g + e] >> nsh) & 0x0f0f0f0fu;
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    v[4 * e + k] = vkf_to_f16(fmaf(dsc, (float)((n >> (8 * k)) & 0xffu), -dm));
+            }
+            out[g] = live ? __builtin_bit_cast(vkf_i4, v) : vkf_i4{0, 0, 0, 0};
+        }
+    }
+};
+
+// Q6_K: half h (elements 16h .. 16h+15, one scale) of 32-element block t of
+// half ip: ql bytes 64ip + 32(t&1) + 16h .., qh bytes 128 + 32ip + 16h ..,
+// each loaded as the five aligned dwords that cover it (inside the
+// super-block) and realigned.
+template <>
+struct QHalf<VKF_Q6_K> {
+    uint32_t ql[5], qh[5], sc, dd, sh, t, h;
+    bool live;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        const uint32_t rw = row0 + (threadIdx.x >> 2), kc = k0 + 32 * ((threadIdx.x >> 1) & 1);
+        h = threadIdx.x & 1;
+        live = rw < nrows && kc < K;
+        const uint32_t kk = kc < K ? kc : 0, j8 = (kk % 256) / 32, ip = j8 >> 2;
+        t = j8 & 3;
+        const uint8_t *blk = W + (uint64_t)(rw < nrows ? rw : nrows - 1) * row_bytes + 210ull * (kk / 256);
+        sh = (uint32_t)(uintptr_t)blk & 3u;
+        const uint8_t *a = blk - sh;  // 4-byte aligned
+        const uint8_t *pl = a + 64 * ip + 32 * (t & 1) + 16 * h, *ph = a + 128 + 32 * ip + 16 * h;
+        const vkf_u4 l0 = *(const vkf_u4a4 *)pl, h0 = *(const vkf_u4a4 *)ph;
+        ql[0] = l0[0]; ql[1] = l0[1]; ql[2] = l0[2]; ql[3] = l0[3];
+        qh[0] = h0[0]; qh[1] = h0[1]; qh[2] = h0[2]; qh[3] = h0[3];
+        ql[4] = *(const uint32_t *)(pl + 16);  // ends at byte <= 132 of the super-block
+        qh[4] = *(const uint32_t *)(ph + 16);  // ends at byte <= 196
+        sc = *(const uint16_t *)(blk + 192 + 8 * ip + 2 * t);
+        dd = *(const uint16_t *)(blk + 208);
+    }
+    __device__ __forceinline__ void decode(vkf_i4 out[2]) {
+        const float d = vkf_h2f((uint16_t)dd);
+        const float ds = d * (float)(int8_t)(h ? (sc >> 8) : (sc & 0xffu)), off = -32.0f * ds;
+        const uint32_t nsh = 4 * (t >> 1), hsh = 2 * t;
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            vkf_h8 v;
+#pragma unroll
+            for (int e2 = 0; e2 < 2; e2++) {
+                const int i = 2 * g + e2;
+                const uint32_t l = realign(ql[i], ql[i + 1], sh), hb = realign(qh[i], qh[i + 1], sh);
+                const uint32_t u = ((l >> nsh) & 0x0f0f0f0fu) | (((hb >> hsh) & 0x03030303u) << 4);
+#pragma unroll
+                for (int k = 0; k < 4; k++) v[4 * e2 + k] = vkf_to_f16(fmaf(ds, (float)((u >> (8 * k)) & 0xffu), off));
+            }
+            out[g] = live ? __builtin_bit_cast(vkf_i4, v) : vkf_i4{0, 0, 0, 0};
+        }
+    }
+};
+
+template <int QT> constexpr bool has_qhalf() { return QT == VKF_Q4_K || QT == VKF_Q6_K; }
 // Both operands quantised (Q8_1 activations x ggml weights): both tiles are
 // staged through registers with the same load-before / decode-after split.
 template <int XQT, int QT>
@@ -910,6 +1005,39 @@ __device__ __forceinline__ void gemm_mainloop_wide(const VkfGemmArgs &a, uint32_
 #pragma unroll
         for (int g = 0; g < 4; g++) *(vkf_i4 *)(sy + (((4 * yh + g) ^ (yr & 7)) << 4)) = t.v[g];
     };
+    if constexpr (has_qhalf<QT>()) {
+        // all eight waves decode: thread t -> row t/4, elements 16(t&3) ..
+        const uint32_t hr = threadIdx.x >> 2, hq = threadIdx.x & 3;
+        auto store_h = [&](uint32_t stage, const vkf_i4 v[2]) {
+            uint8_t *sy = smem + stage * GEMM_W_STAGE + 32768 + hr * 128;
+#pragma unroll
+            for (int g = 0; g < 2; g++) *(vkf_i4 *)(sy + (((2 * hq + g) ^ (hr & 7)) << 4)) = v[g];
+        };
+        QHalf<QT> q;
+        vkf_i4 tv[2];
+        issue_x(0, 0);
+        q.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, 0);
+        q.decode(tv);
+        store_h(0, tv);
+        wait_vm<0>();
+        __syncthreads();
+        for (uint32_t kt = 0; kt < nk; kt++) {
+            const uint32_t cur = kt & 1;
+            if (kt + 1 < nk) {
+                issue_x(kt + 1, cur ^ 1);
+                q.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, (kt + 1) * 64);
+            }
+            const uint8_t *lx = smem + cur * GEMM_W_STAGE;
+            mfma_step_swz<2>(lx, lx + 32768, wr, wc, acc);
+            if (kt + 1 < nk) {
+                q.decode(tv);
+                store_h(cur ^ 1, tv);
+            }
+            wait_vm<0>();
+            __syncthreads();
+        }
+        return;
+    }
     QStage<QT> q;
     TileRegs ty;
     issue_x(0, 0);
