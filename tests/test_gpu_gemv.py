@@ -140,7 +140,7 @@ def test_config5_q6_k_q8_1_gemv(dev):
     assert _rows_check(y, x64, w, O.Q6_K, K, rows) <= TOL_F32
 
 
-DOT_TYPES = [O.Q4_0, O.Q4_1, O.Q8_0, O.Q4_K]
+DOT_TYPES = [O.Q4_0, O.Q4_1, O.Q8_0, O.Q4_K, O.Q5_K]
 
 
 def _per_row_err(y, x64, w, qt, N, K):
@@ -222,7 +222,7 @@ def test_gemv_mfma(dev, qt, M, N, K):
     assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32
 
 
-@pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_1, O.Q4_K], ids=["q4_0", "q4_1", "q4_k"])
+@pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_1, O.Q4_K, O.Q5_K], ids=["q4_0", "q4_1", "q4_k", "q5_k"])
 @pytest.mark.parametrize("kind", ["f16", "f32"])
 @pytest.mark.parametrize("NK", [(77, 1600), (77, 1664), (77, 1728), (3001, 4096), (100003, 2624)],
                          ids=["77x1600", "77x1664", "77x1728", "3001x4096", "100003x2624"])
@@ -232,8 +232,8 @@ def test_gemv_dot_lds_tails(dev, qt, kind, NK):
     middle of a multi-iteration row walk), checked on a spread of rows."""
     from vkflame_amd import ops
     N, K = NK
-    if qt == O.Q4_K and K % 256:
-        pytest.skip("Q4_K rows are whole 256-element super-blocks")
+    if qt in (O.Q4_K, O.Q5_K) and K % 256:
+        pytest.skip("K-quant rows are whole 256-element super-blocks")
     w = O.gen_weight(qt, N, K, seed_for(2, 80 + qt))
     xa, x64 = _x(kind, 1, K, seed_for(2, 81))
     y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
@@ -252,3 +252,23 @@ def test_stream_read_hook(dev):
         ops.stream_read(buf, sink)
     torch.cuda.synchronize()
     assert int(sink.item()) == 7
+
+
+@pytest.mark.parametrize("qt", [O.Q4_K, O.Q5_K], ids=["q4_k", "q5_k"])
+@pytest.mark.parametrize("M", [1, 3])
+def test_gemv_dot_largest_codes(dev, qt, M):
+    """Every code at its maximum (15 / 31), every 6-bit scale and min 63 and
+    activations that quantise to the largest integers: the dot GEMV's integer
+    products reach their bound (|sc * P| < 2^31 for Q5_K) without overflow."""
+    from vkflame_amd import ops
+    N, K = 300, 4096
+    w = O.gen_weight(qt, N, K, seed_for(2, 90 + qt)).reshape(-1, O.BLOCK_BYTES[qt])
+    w[:, 4:16] = 0xFF                      # scales / mins: all 63
+    w[:, 16:] = 0xFF                       # (Q5_K qh and) qs: every code at its maximum
+    w = w.reshape(N, -1)
+    x = np.ones((M, K), np.float32)
+    x[:, 1::2] = -1.0 if M == 1 else 1.0
+    xa = x.astype(np.float16)
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
+    ref = O.ref_gemv(x.astype(np.float64), O.np_dequant(qt, w.reshape(-1)).reshape(N, K))
+    assert rel_err(y, ref) <= TOL_F32

@@ -57,9 +57,10 @@ VkfKernelId gemm_kernel(int qt, int xk) {
     return VKF_K_COUNT;
 }
 
-// Dot-product GEMV (kernels/gemv_dot.hip): Q4_0, Q4_1, Q8_0, Q4_K weights,
-// fp16 / fp32 activations, M <= 4.  Chunks are 64 elements; the chunk loads
-// need the row starts aligned as below (36-, 40-, 68- and 144-byte chunks).
+// Dot-product GEMV (kernels/gemv_dot.hip): Q4_0, Q4_1, Q8_0, Q4_K, Q5_K
+// weights, fp16 / fp32 activations, M <= 4.  Chunks are 64 elements; the
+// chunk loads need the row starts aligned as below (36-, 40-, 68-, 144- and
+// 176-byte chunk groups).
 constexpr int kDotWaves = 16;
 // LDS image per workgroup: 8 planes of 4 KiB per reserved activation row
 // plus a 4 KiB table of per-chunk scales and sums (kernels/gemv_dot.hip),
@@ -78,10 +79,11 @@ int dot_format(int qt) {
     case VKF_Q4_1: return 1;
     case VKF_Q8_0: return 2;
     case VKF_Q4_K: return 3;
+    case VKF_Q5_K: return 4;
     default: return -1;
     }
 }
-const uint32_t kDotAlign[4] = {4, 8, 4, 16};
+const uint32_t kDotAlign[5] = {4, 8, 4, 16, 16};
 
 // Lanes per row segment.  A wave tile is (64/S)*rpl rows; a lane walks
 // ceil(C/S) chunks per tile and a wave ceil(tiles/slots) tiles, so the
@@ -241,10 +243,10 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
             return 0;
         }
         const int fi = dot_format(qt);
-        // M = 1, Q4_0 / Q4_1 / Q4_K: the dot GEMV with the weights fetched
+        // M = 1, Q4_0 / Q4_1 / Q4_K / Q5_K: the dot GEMV with the weights fetched
         // into LDS by contiguous direct loads (kernels/gemv_dot.hip
         // gemv_dot_lds): two 3 KiB buffers per wave next to the activations
-        const int li = qt == VKF_Q4_0 ? 0 : qt == VKF_Q4_1 ? 1 : qt == VKF_Q4_K ? 2 : -1;
+        const int li = qt == VKF_Q4_0 ? 0 : qt == VKF_Q4_1 ? 1 : qt == VKF_Q4_K ? 2 : qt == VKF_Q5_K ? 3 : -1;
         if (li >= 0 && M == 1 && xk != 2 && (K % 64) == 0 && K <= kDotMaxK && kDotLdsL <= vkf::max_lds() &&
             aligned(w, kDotAlign[fi]) && (row_bytes % kDotAlign[fi]) == 0) {
             const uint32_t cus = (uint32_t)vkf::cu_count();

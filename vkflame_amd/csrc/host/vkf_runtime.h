@@ -62,6 +62,8 @@
     X(GEMV_DOTL_Q4_1_F32, "vkf_gemv_dotl_q4_1_f32")        \
     X(GEMV_DOTL_Q4_K_F16, "vkf_gemv_dotl_q4_k_f16")        \
     X(GEMV_DOTL_Q4_K_F32, "vkf_gemv_dotl_q4_k_f32")        \
+    X(GEMV_DOTL_Q5_K_F16, "vkf_gemv_dotl_q5_k_f16")        \
+    X(GEMV_DOTL_Q5_K_F32, "vkf_gemv_dotl_q5_k_f32")        \
     X(GEMV_MFMA_Q4_K_F16, "vkf_gemv_mfma_q4_k_f16")        \
     X(GEMV_MFMA_Q4_0_F16, "vkf_gemv_mfma_q4_0_f16")        \
     X(GEMV_MFMA_Q4_1_F16, "vkf_gemv_mfma_q4_1_f16")        \
@@ -82,6 +84,10 @@
     X(GEMV_DOT_Q4_K_F32_M1, "vkf_gemv_dot_q4_k_f32_m1") \
     X(GEMV_DOT_Q4_K_F16_M4, "vkf_gemv_dot_q4_k_f16_m4") \
     X(GEMV_DOT_Q4_K_F32_M4, "vkf_gemv_dot_q4_k_f32_m4") \
+    X(GEMV_DOT_Q5_K_F16_M1, "vkf_gemv_dot_q5_k_f16_m1") \
+    X(GEMV_DOT_Q5_K_F32_M1, "vkf_gemv_dot_q5_k_f32_m1") \
+    X(GEMV_DOT_Q5_K_F16_M4, "vkf_gemv_dot_q5_k_f16_m4") \
+    X(GEMV_DOT_Q5_K_F32_M4, "vkf_gemv_dot_q5_k_f32_m4") \
     X(GEMM_F16, "vkf_gemm_f16")                             \
     X(GEMM_I8, "vkf_gemm_i8")                               \
     /* GEMM: fp16 and Q8_1 activations per weight type */   \

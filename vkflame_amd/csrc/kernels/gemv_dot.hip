@@ -179,7 +179,8 @@ template <> struct DotFmt<VKF_Q4_0> {
         k.d[0] = h_lo(r[0]);
         k.d[1] = h_hi(r[4]);
     }
-    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t w[8]) {
+    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t il, uint32_t w[8]) {
+        (void)il;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             // block 0: qs at bytes 2..17, block 1: bytes 20..35
@@ -216,7 +217,8 @@ template <> struct DotFmt<VKF_Q4_1> {
             k.m[b] = h_hi(r[5 * b]);
         }
     }
-    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t w[8]) {
+    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t il, uint32_t w[8]) {
+        (void)il;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t q = r[5 * b + 1 + i];
@@ -253,7 +255,8 @@ template <> struct DotFmt<VKF_Q8_0> {
         k.d[0] = h_lo(r[0]);
         k.d[1] = h_hi(r[8]);
     }
-    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t w[8]) {
+    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t il, uint32_t w[8]) {
+        (void)il;
 #pragma unroll
         for (int i = 0; i < 8; i++)  // block 0: qs at bytes 2..33, block 1: bytes 36..67
             w[i] = b == 0 ? __builtin_amdgcn_alignbyte(r[i + 1], r[i], 2) : r[9 + i];
@@ -297,7 +300,8 @@ template <> struct DotFmt<VKF_Q4_K> {
         k.mn[0] = (int)((mnW >> sh) & 0xffu);
         k.mn[1] = (int)((mnW >> (sh + 8)) & 0xffu);
     }
-    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t w[8]) {
+    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t il, uint32_t w[8]) {
+        (void)il;
 #pragma unroll
         for (int i = 0; i < 8; i++) w[i] = b == 0 ? nib_lo(r[4 + i]) : nib_hi(r[4 + i]);
     }
@@ -306,6 +310,42 @@ template <> struct DotFmt<VKF_Q4_K> {
     // (|mS| < 2^25), all factors within the 24-bit multiplier's range.
     static __device__ __forceinline__ float fold(const K &k, int P0, int P1, float fe, int S0, int S1, float acc) {
         const int Q = __mul24(k.sc[0], P0) + __mul24(k.sc[1], P1);
+        const int mS = __mul24(k.mn[0], S0) + __mul24(k.mn[1], S1);
+        return fmaf(fe, fmaf(k.dall, (float)Q, -k.dmin * (float)mS), acc);
+    }
+};
+
+// Q5_K: 176-byte super-blocks {fp16 dall, fp16 dmin, scales[12], qh[32],
+// qs[128]} (kernels/dequant_q5_k.glsl:34-42, 51-73): as Q4_K, with the 5th
+// bit of element l of chunk il in qh[l], bit 2il (low nibbles, sub-block 2il)
+// or 2il+1 (high nibbles).  Codes 0..31; scales, mins and fold as Q4_K, the
+// integer products in full 32-bit (|sc*P| < 2^31, beyond __mul24's range).
+template <> struct DotFmt<VKF_Q5_K> {
+    static constexpr int NW = 20;
+    using K = DotFmt<VKF_Q4_K>::K;
+    static __device__ __forceinline__ void load(const uint8_t *row, uint32_t c, uint32_t r[NW]) {
+        const uint8_t *b = row + 176u * (c >> 2);
+        const vkf_u4 h = *(const vkf_u4 *)b, q0 = *(const vkf_u4 *)(b + 16), q1 = *(const vkf_u4 *)(b + 32);
+        const vkf_u4 s0 = *(const vkf_u4 *)(b + 48 + 32u * (c & 3)), s1 = *(const vkf_u4 *)(b + 64 + 32u * (c & 3));
+        r[0] = h[0]; r[1] = h[1]; r[2] = h[2]; r[3] = h[3];
+        r[4] = q0[0]; r[5] = q0[1]; r[6] = q0[2]; r[7] = q0[3];
+        r[8] = q1[0]; r[9] = q1[1]; r[10] = q1[2]; r[11] = q1[3];
+        r[12] = s0[0]; r[13] = s0[1]; r[14] = s0[2]; r[15] = s0[3];
+        r[16] = s1[0]; r[17] = s1[1]; r[18] = s1[2]; r[19] = s1[3];
+    }
+    static __device__ __forceinline__ void consts(const uint32_t r[NW], uint32_t il, K &k) {
+        DotFmt<VKF_Q4_K>::consts(r, il, k);  // header words r[0..3], same layout
+    }
+    static __device__ __forceinline__ void codes(const uint32_t r[NW], int b, uint32_t il, uint32_t w[8]) {
+        const uint32_t hs = 2 * il + (uint32_t)b;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t q = b == 0 ? nib_lo(r[12 + i]) : nib_hi(r[12 + i]);
+            w[i] = q | (((r[4 + i] >> hs) & 0x01010101u) << 4);
+        }
+    }
+    static __device__ __forceinline__ float fold(const K &k, int P0, int P1, float fe, int S0, int S1, float acc) {
+        const int Q = k.sc[0] * P0 + k.sc[1] * P1;
         const int mS = __mul24(k.mn[0], S0) + __mul24(k.mn[1], S1);
         return fmaf(fe, fmaf(k.dall, (float)Q, -k.dmin * (float)mS), acc);
     }
@@ -395,7 +435,7 @@ __device__ __forceinline__ void gemv_dot(const VkfGemvArgs &a) {
                         for (int b = 0; b < 2; b++) {
                             uint32_t w[RPL][8];
 #pragma unroll
-                            for (int j = 0; j < RPL; j++) F::codes(raw[d][j], b, w[j]);
+                            for (int j = 0; j < RPL; j++) F::codes(raw[d][j], b, il, w[j]);
 #pragma unroll
                             for (int m = 0; m < MM; m++) {
                                 if (MM == 1 || m < (int)M) {
@@ -459,8 +499,8 @@ __device__ __forceinline__ void gemv_dot(const VkfGemvArgs &a) {
 // valid bytes are loaded again into registers and written over it.
 // Dynamic LDS: dot_lds_bytes<1>() + DOT_WAVES * 2 * DOT_WBUF.
 // ---------------------------------------------------------------------------
-template <int QT> constexpr uint32_t dot_cb() { return QT == VKF_Q4_1 ? 40 : 36; }
-#define DOT_NLD 3  // direct loads per lane per iteration (3 x 64 >= 4 * 40)
+template <int QT> constexpr uint32_t dot_cb() { return QT == VKF_Q4_1 ? 40 : QT == VKF_Q5_K ? 44 : 36; }
+#define DOT_NLD 3  // direct loads per lane per iteration (3 x 64 >= 4 * 44)
 #define DOT_WBUF (DOT_NLD * 64 * 16)
 
 template <int QT, int XK, uint32_t S>
@@ -553,7 +593,7 @@ __device__ __forceinline__ void gemv_dot_lds(const VkfGemvArgs &a, unsigned char
 #pragma unroll
                 for (int b = 0; b < 2; b++) {
                     uint32_t w[8];
-                    F::codes(raw, b, w);
+                    F::codes(raw, b, il, w);
                     P[b] = group_dot(w, smem + (b * 4) * DOT_PLANE + c * 16);
                 }
                 const vkf_i4 xs = *(const vkf_i4 *)(smem + xs_offset<1>(0, c));
@@ -608,8 +648,9 @@ VKF_GEMV_DOT(q4_0, VKF_Q4_0)
 VKF_GEMV_DOT(q4_1, VKF_Q4_1)
 VKF_GEMV_DOT(q8_0, VKF_Q8_0)
 VKF_GEMV_DOT(q4_k, VKF_Q4_K)
+VKF_GEMV_DOT(q5_k, VKF_Q5_K)
 
-// M = 1 through LDS: vkf_gemv_dotl_{q4_0,q4_1,q4_k}_{f16,f32}
+// M = 1 through LDS: vkf_gemv_dotl_{q4_0,q4_1,q4_k,q5_k}_{f16,f32}
 #define VKF_GEMV_DOTL(name, QT)                                                                         \
     VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dotl_##name##_f16(VkfGemvArgs a) {       \
         gemv_dot_lds_entry<QT, 0>(a);                                                                   \
@@ -620,3 +661,4 @@ VKF_GEMV_DOT(q4_k, VKF_Q4_K)
 VKF_GEMV_DOTL(q4_0, VKF_Q4_0)
 VKF_GEMV_DOTL(q4_1, VKF_Q4_1)
 VKF_GEMV_DOTL(q4_k, VKF_Q4_K)
+VKF_GEMV_DOTL(q5_k, VKF_Q5_K)
