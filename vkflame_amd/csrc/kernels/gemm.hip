@@ -402,6 +402,54 @@ struct QStage<VKF_Q4_K> {
     }
 };
 
+// Q5_K: as Q4_K with the fifth bit of element l of sub-block j in qh[l], bit
+// j (kernels/dequant_q5_k.glsl:51-73; 176-byte super-blocks: header, qh[32]
+// at 16, qs[128] at 48).  Value fma(dall*sc, q, -dmin*m) in fp32 (exact up to
+// the one rounding), then fp16.
+template <>
+struct QStage<VKF_Q5_K> {
+    vkf_u4 hdr, qa, qb, ha, hb;
+    uint32_t j;
+    bool live;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        const uint32_t r = row0 + (threadIdx.x >> 1), kc = k0 + 32 * (threadIdx.x & 1);
+        live = r < nrows && kc < K;
+        const uint32_t rr = r < nrows ? r : nrows - 1, kk = kc < K ? kc : 0;
+        const uint8_t *blk = W + (uint64_t)rr * row_bytes + 176ull * (kk / 256);
+        j = (kk % 256) / 32;
+        hdr = *(const vkf_u4a4 *)blk;
+        ha = *(const vkf_u4a4 *)(blk + 16);
+        hb = *(const vkf_u4a4 *)(blk + 32);
+        const uint8_t *q = blk + 48 + 32 * (j >> 1);
+        qa = *(const vkf_u4a4 *)q;
+        qb = *(const vkf_u4a4 *)(q + 16);
+    }
+    __device__ __forceinline__ void decode(TileRegs &out) {
+        const float dall = vkf_h2f(hdr[0] & 0xffffu), dmin = vkf_h2f(hdr[0] >> 16);
+        const uint32_t s0 = hdr[1], s4 = hdr[2], s8 = hdr[3];
+        const uint32_t scW = j < 4 ? (s0 & 0x3f3f3f3fu) : ((s8 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u));
+        const uint32_t mnW = j < 4 ? (s4 & 0x3f3f3f3fu) : (((s8 >> 4) & 0x0f0f0f0fu) | ((s4 >> 2) & 0x30303030u));
+        const uint32_t sh = 8 * (j & 3);
+        const float dsc = dall * (float)((scW >> sh) & 0xffu), dm = dmin * (float)((mnW >> sh) & 0xffu);
+        const uint32_t nsh = 4 * (j & 1);
+        const uint32_t w[8] = {qa[0], qa[1], qa[2], qa[3], qb[0], qb[1], qb[2], qb[3]};
+        const uint32_t hq[8] = {ha[0], ha[1], ha[2], ha[3], hb[0], hb[1], hb[2], hb[3]};
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            vkf_h8 h;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t n = ((w[2 * g + e] >> nsh) & 0x0f0f0f0fu) | (((hq[2 * g + e] >> j) & 0x01010101u) << 4);
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    h[4 * e + k] = vkf_to_f16(fmaf(dsc, (float)((n >> (8 * k)) & 0xffu), -dm));
+            }
+            out.v[g] = live ? __builtin_bit_cast(vkf_i4, h) : vkf_i4{0, 0, 0, 0};
+        }
+    }
+};
+
 // 32-element blocks at 2-byte aligned addresses (Q4_0 18 B, Q8_0 34 B): the
 // block's bytes are loaded as the 4-byte aligned dwords that cover them and
 // realigned by sh = block address & 3 (0 or 2); no load reaches past the
@@ -645,6 +693,48 @@ struct QHalf<VKF_Q4_K> {
     }
 };
 
+// Q5_K: half h of sub-block j: qs bytes 48 + 32(j/2) + 16h .., qh bytes 16 +
+// 16h .. (bit j), as QStage<VKF_Q5_K>.
+template <>
+struct QHalf<VKF_Q5_K> {
+    vkf_u4 hdr, qs, qh;
+    uint32_t j;
+    bool live;
+    __device__ __forceinline__ void load(const uint8_t *W, uint64_t row_bytes, uint32_t nrows, uint32_t row0,
+                                         uint32_t K, uint32_t k0) {
+        const uint32_t r = row0 + (threadIdx.x >> 2), kc = k0 + 32 * ((threadIdx.x >> 1) & 1);
+        const uint32_t h = threadIdx.x & 1;
+        live = r < nrows && kc < K;
+        const uint32_t rr = r < nrows ? r : nrows - 1, kk = kc < K ? kc : 0;
+        const uint8_t *blk = W + (uint64_t)rr * row_bytes + 176ull * (kk / 256);
+        j = (kk % 256) / 32;
+        hdr = *(const vkf_u4a4 *)blk;
+        qh = *(const vkf_u4a4 *)(blk + 16 + 16 * h);
+        qs = *(const vkf_u4a4 *)(blk + 48 + 32 * (j >> 1) + 16 * h);
+    }
+    __device__ __forceinline__ void decode(vkf_i4 out[2]) {
+        const float dall = vkf_h2f(hdr[0] & 0xffffu), dmin = vkf_h2f(hdr[0] >> 16);
+        const uint32_t s0 = hdr[1], s4 = hdr[2], s8 = hdr[3];
+        const uint32_t scW = j < 4 ? (s0 & 0x3f3f3f3fu) : ((s8 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u));
+        const uint32_t mnW = j < 4 ? (s4 & 0x3f3f3f3fu) : (((s8 >> 4) & 0x0f0f0f0fu) | ((s4 >> 2) & 0x30303030u));
+        const uint32_t sh = 8 * (j & 3);
+        const float dsc = dall * (float)((scW >> sh) & 0xffu), dm = dmin * (float)((mnW >> sh) & 0xffu);
+        const uint32_t nsh = 4 * (j & 1);
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            vkf_h8 v;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t n = ((qs[2 * g + e] >> nsh) & 0x0f0f0f0fu) | (((qh[2 * g + e] >> j) & 0x01010101u) << 4);
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    v[4 * e + k] = vkf_to_f16(fmaf(dsc, (float)((n >> (8 * k)) & 0xffu), -dm));
+            }
+            out[g] = live ? __builtin_bit_cast(vkf_i4, v) : vkf_i4{0, 0, 0, 0};
+        }
+    }
+};
+
 // Q6_K: half h (elements 16h .. 16h+15, one scale) of 32-element block t of
 // half ip: ql bytes 64ip + 32(t&1) + 16h .., qh bytes 128 + 32ip + 16h ..,
 // each loaded as the five aligned dwords that cover it (inside the
@@ -692,7 +782,7 @@ struct QHalf<VKF_Q6_K> {
     }
 };
 
-template <int QT> constexpr bool has_qhalf() { return QT == VKF_Q4_K || QT == VKF_Q6_K; }
+template <int QT> constexpr bool has_qhalf() { return QT == VKF_Q4_K || QT == VKF_Q5_K || QT == VKF_Q6_K; }
 // Both operands quantised (Q8_1 activations x ggml weights): both tiles are
 // staged through registers with the same load-before / decode-after split.
 template <int XQT, int QT>
