@@ -272,3 +272,24 @@ def test_gemv_dot_largest_codes(dev, qt, M):
     y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
     ref = O.ref_gemv(x.astype(np.float64), O.np_dequant(qt, w.reshape(-1)).reshape(N, K))
     assert rel_err(y, ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("kind", ["f16", "f32"])
+@pytest.mark.parametrize("N", [1, 77, 3001, 20011])
+@pytest.mark.parametrize("K", [2048, 4608, 5120, 16384])
+def test_gemv_q6k_float_activations(dev, kind, N, K):
+    """Q6_K x fp16 / fp32 activations at M = 1: the Q6_K integer GEMV with the
+    activations split into two int8 rows per 32-element block (x ~ dh*qh +
+    dl*ql, error <= max|x|/(4*127*127) per block), checked against the
+    float64 product of the exact fp16 / fp32 activations; rows whose tails end
+    0, 4, 8 or 12 bytes into a 16-byte piece, every row-segment width, scales
+    over the whole int8 range."""
+    from vkflame_amd import ops
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(5, 20 + N % 7)).reshape(-1, 210)
+    rng = np.random.default_rng(seed_for(5, 21))
+    w[::3, 192:208] = rng.integers(-128, 128, (w[::3].shape[0], 16)).astype(np.int8).view(np.uint8)
+    w = w.reshape(N, -1)
+    xa, x64 = _x(kind, 1, K, seed_for(5, 22))
+    y = ops.gemm_q(to_dev(w, dev), O.Q6_K, to_dev(xa, dev), N, K).cpu().numpy()
+    rows = np.unique(np.concatenate([np.arange(0, N, max(1, N // 150)), [N - 1]]))
+    assert _rows_check(y, x64, w, O.Q6_K, K, rows) <= TOL_F32

@@ -72,6 +72,9 @@ constexpr size_t kDotLdsL = kDotLdsM1 + 16 * 2 * 3 * 1024;
 // kernels/gemv_q6k.hip, one activation row: x planes + two weight buffers
 // for each of its 8 waves
 constexpr size_t kDotLdsQ6 = 11 * 4096 + 8 * 2 * 7 * 1024;
+// the same kernel with fp16 / fp32 activations split into two int8 rows:
+// two 11-plane images of up to 128 chunks (K <= 16384)
+constexpr size_t kDotLdsQ6x = 2 * 11 * 2048 + 8 * 2 * 7 * 1024;
 constexpr int kQ6Waves = 8;
 int dot_format(int qt) {
     switch (qt) {
@@ -276,6 +279,17 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
             a.flags |= seg << 8;
             return vkf::launch(VKF_K_GEMV_Q6K_Q81_DOT_M1, dim3(tiles < cus ? tiles : cus), dim3(64 * kQ6Waves), a,
                                S(stream), kDotLdsQ6);
+        }
+        // Q6_K x fp16 / fp32 at M = 1: the same kernel, the activations split
+        // into two int8 rows (hi and residual) staged in LDS and summed
+        if (qt == VKF_Q6_K && xk != 2 && M == 1 && K <= 128 * 128 && aligned(w, 4) && (row_bytes % 4) == 0 &&
+            kDotLdsQ6x <= vkf::max_lds()) {
+            const uint32_t cus = (uint32_t)vkf::cu_count();
+            const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 128), 1, cus * kQ6Waves);
+            const uint32_t tiles = cdiv(N, 64 / seg);
+            a.flags |= seg << 8;
+            return vkf::launch(xk == 0 ? VKF_K_GEMV_Q6K_F16_DOT_M1 : VKF_K_GEMV_Q6K_F32_DOT_M1,
+                               dim3(tiles < cus ? tiles : cus), dim3(64 * kQ6Waves), a, S(stream), kDotLdsQ6x);
         }
         return vkf::launch(gemv_kernel(qt, xk), dim3(cdiv(N, 4)), dim3(256), a, S(stream));
     }

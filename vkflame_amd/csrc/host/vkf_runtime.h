@@ -56,6 +56,8 @@
     X(GEMV_Q6_K_Q81, "vkf_gemv_q6_k_q8_1_int")              \
     X(Q6_K_Q8_1_PARTIALS, "vkf_q6_k_q8_1_partials")         \
     X(GEMV_Q6K_Q81_DOT_M1, "vkf_gemv_q6k_q81_dot_m1")      \
+    X(GEMV_Q6K_F16_DOT_M1, "vkf_gemv_q6k_f16_dot_m1")      \
+    X(GEMV_Q6K_F32_DOT_M1, "vkf_gemv_q6k_f32_dot_m1")      \
     X(GEMV_DOTL_Q4_0_F16, "vkf_gemv_dotl_q4_0_f16")        \
     X(GEMV_DOTL_Q4_0_F32, "vkf_gemv_dotl_q4_0_f32")        \
     X(GEMV_DOTL_Q4_1_F16, "vkf_gemv_dotl_q4_1_f16")        \

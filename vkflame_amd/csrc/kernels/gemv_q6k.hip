@@ -70,6 +70,54 @@ __device__ __forceinline__ void q6_stage_block(const VkfGemvArgs &a, unsigned ch
     ((int *)q6_plane<MM>(lds, m, 10, c))[t] = x1;
 }
 
+// fp16 / fp32 activations at M = 1 (XK 0 / 1): block kb of x (32 values)
+// as two int8 rows with fp32 scales, x ~ dh*qh + dl*ql: rows 0 and 1 of the
+// LDS image.  qh = round(x/dh) with dh = max|x|/127, ql the same of the
+// residual x - dh*qh (|x - dh*qh - dl*ql| <= dl/2 <= max|x|/(4*127*127)),
+// so the integer dot products of the two rows, summed, carry x to ~16 bits.
+template <int XK>
+__device__ __forceinline__ void q6_stage_split(const VkfGemvArgs &a, unsigned char *lds, uint32_t kb) {
+    float x[32];
+    if (XK == 1) {
+        const vkf_f4 *p = (const vkf_f4 *)((const float *)a.x + 32ull * kb);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const vkf_f4 v = p[i];
+            x[4 * i] = v[0]; x[4 * i + 1] = v[1]; x[4 * i + 2] = v[2]; x[4 * i + 3] = v[3];
+        }
+    } else {
+        const vkf_h8 *p = (const vkf_h8 *)((const _Float16 *)a.x + 32ull * kb);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const vkf_h8 v = p[i];
+#pragma unroll
+            for (int j = 0; j < 8; j++) x[8 * i + j] = (float)v[j];
+        }
+    }
+    const uint32_t c = kb >> 2, t = kb & 3;
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(x[i]));
+        const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int x0 = 0, x1 = 0;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const int v = (int)rintf(x[i] * id);  // |v| <= 127
+            x[i] = fmaf(-d, (float)v, x[i]);       // residual for the next row
+            q[i >> 2] |= ((uint32_t)v & 0xffu) << (8 * (i & 3));
+            if (i < 16) x0 += v; else x1 += v;
+        }
+        *(vkf_u4 *)q6_plane<2>(lds, m, 2 * t, c) = vkf_u4{q[0], q[1], q[2], q[3]};
+        *(vkf_u4 *)q6_plane<2>(lds, m, 2 * t + 1, c) = vkf_u4{q[4], q[5], q[6], q[7]};
+        ((float *)q6_plane<2>(lds, m, 8, c))[t] = d;
+        ((int *)q6_plane<2>(lds, m, 9, c))[t] = x0;
+        ((int *)q6_plane<2>(lds, m, 10, c))[t] = x1;
+    }
+}
+
 // Raw dwords of one chunk: ql 17, qh 9, sc 3 (one extra dword each for the
 // realignment), and the fp16 d.  Every load stays inside the chunk's
 // super-block: the dwords beyond byte 209 that an even super-block would
@@ -151,9 +199,9 @@ __device__ __forceinline__ float q6_chunk(const Q6Raw &r, uint32_t sh, const uns
 // flags bit 0: y += instead of y =; bits 8..15: S (lanes per row segment,
 // a power of two 8..64).  Dynamic LDS: MM * 11 * q6_plane_bytes<MM>() +
 // Q6_WAVES * 2 * Q6_WBUF.  row_bytes % 4 == 0 and K >= 256 (host).
-template <int MM, uint32_t S>
+template <int MM, uint32_t S, int XS = -1>
 __device__ __forceinline__ void gemv_q6k_q81(const VkfGemvArgs &a, unsigned char *smem) {
-    const uint32_t C = a.K / 128, M = a.M, nkb = a.K / 32;
+    const uint32_t C = a.K / 128, M = XS >= 0 ? 2 : a.M, nkb = a.K / 32;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t seg = lane / S, p = lane & (S - 1);
@@ -165,9 +213,13 @@ __device__ __forceinline__ void gemv_q6k_q81(const VkfGemvArgs &a, unsigned char
     unsigned char *wb = smem + MM * 11 * q6_plane_bytes<MM>() + wave * 2 * Q6_WBUF;
     const uint32_t last = (uint32_t)a.row_bytes - 16;  // last 16-byte piece of a row (row_bytes % 4 == 0)
 
-    for (uint32_t i = threadIdx.x; i < M * nkb; i += blockDim.x) {
-        const uint32_t m = i / nkb;
-        q6_stage_block<MM>(a, smem, m, i - m * nkb);
+    if constexpr (XS >= 0) {
+        for (uint32_t i = threadIdx.x; i < nkb; i += blockDim.x) q6_stage_split<XS>(a, smem, i);
+    } else {
+        for (uint32_t i = threadIdx.x; i < M * nkb; i += blockDim.x) {
+            const uint32_t m = i / nkb;
+            q6_stage_block<MM>(a, smem, m, i - m * nkb);
+        }
     }
     __syncthreads();
 
@@ -242,8 +294,9 @@ __device__ __forceinline__ void gemv_q6k_q81(const VkfGemvArgs &a, unsigned char
                     if (MM == 1 || m < (int)M) acc[m] += q6_chunk<MM>(r, sh, smem, m, c);
             }
         }
+        if constexpr (XS >= 0) acc[0] += acc[1];  // the two rows of x sum to x
 #pragma unroll
-        for (int m = 0; m < MM; m++) {
+        for (int m = 0; m < (XS >= 0 ? 1 : MM); m++) {
             float v = acc[m];
             for (uint32_t o = S >> 1; o > 0; o >>= 1) v += __shfl_xor(v, (int)o, 64);
             if (p == 0 && m < (int)M && tile * TR + seg < a.N) {
@@ -263,3 +316,19 @@ VKF_KERNEL void __launch_bounds__(64 * Q6_WAVES) vkf_gemv_q6k_q81_dot_m1(VkfGemv
     default: gemv_q6k_q81<1, 64>(a, smem); break;
     }
 }
+
+// Q6_K x fp16 / fp32 activations at M = 1: x split into two int8 rows in LDS
+// (q6_stage_split), dynamic LDS 2 * 11 * q6_plane_bytes<2>() + Q6_WAVES * 2 *
+// Q6_WBUF, K <= 16384.
+template <int XK>
+__device__ __forceinline__ void gemv_q6k_x_entry(const VkfGemvArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    switch ((a.flags >> 8) & 0xffu) {
+    case 8: gemv_q6k_q81<2, 8, XK>(a, smem); break;
+    case 16: gemv_q6k_q81<2, 16, XK>(a, smem); break;
+    case 32: gemv_q6k_q81<2, 32, XK>(a, smem); break;
+    default: gemv_q6k_q81<2, 64, XK>(a, smem); break;
+    }
+}
+VKF_KERNEL void __launch_bounds__(64 * Q6_WAVES) vkf_gemv_q6k_f16_dot_m1(VkfGemvArgs a) { gemv_q6k_x_entry<0>(a); }
+VKF_KERNEL void __launch_bounds__(64 * Q6_WAVES) vkf_gemv_q6k_f32_dot_m1(VkfGemvArgs a) { gemv_q6k_x_entry<1>(a); }
