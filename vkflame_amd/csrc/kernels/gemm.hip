@@ -170,6 +170,9 @@ __device__ __forceinline__ void mfma_step(const uint8_t *lx, const uint8_t *ly, 
         for (int j = 0; j < 4; j++)
             fb[s][j] = *(const vkf_i4 *)(ly + (wc * 64 + 16 * j + li) * GP + 64 * s + 16 * lg);
     }
+    // raised issue priority for the MFMA burst: when both waves of a SIMD
+    // are ready, this wave's MFMAs go first and the matrix pipe stays fed
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < 2; s++)
 #pragma unroll
@@ -183,6 +186,7 @@ __device__ __forceinline__ void mfma_step(const uint8_t *lx, const uint8_t *ly, 
                 else
                     acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
             }
+    __builtin_amdgcn_s_setprio(0);
 }
 
 // The pipelined K loop: acc += X[r0.., :] . Y[c0.., :]^T.  The loads of the
@@ -280,6 +284,9 @@ __device__ __forceinline__ void mfma_step_swz(const uint8_t *lx, const uint8_t *
         for (int j = 0; j < 4; j++)
             fb[s][j] = *(const vkf_i4 *)(ly + (wc * 64 + 16 * j + li) * 128 + ((c ^ sw) << 4));
     }
+    // raised issue priority for the MFMA burst: when both waves of a SIMD
+    // are ready, this wave's MFMAs go first and the matrix pipe stays fed
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < 2; s++)
 #pragma unroll
@@ -293,6 +300,7 @@ __device__ __forceinline__ void mfma_step_swz(const uint8_t *lx, const uint8_t *
                 else
                     acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
             }
+    __builtin_amdgcn_s_setprio(0);
 }
 
 template <int ES, class ACC>
