@@ -61,6 +61,59 @@ def test_linear_int8_int32_exact(dev, M, N, K):
     assert np.array_equal(D.cpu().numpy().astype(np.int64), ref)
 
 
+def _dense_shapes():
+    """(M, N, K) cases on both sides of the split-K switch: grids of at most
+    one 128x128 tile per CU take the 512-thread kernel that splits K between
+    two wave groups (odd and even step counts, one step, ragged edges),
+    larger grids the 256-thread kernel."""
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    # K*bytes a multiple of 128 takes the direct-to-LDS kernels: int8 K = 128,
+    # 384, 640 (1, 3, 5 steps); fp16 K = 192, 1088 (3, 17 steps) and the rest
+    small = [(128, 128, 128), (130, 250, 384), (512, 640, 640), (200, 200, 192), (300, 1000, 1088)]
+    big_m = 128 * (cus // 16 + 1)  # (cus/16 + 1) x 16 tiles > cus
+    big = [(big_m, 2048, 256), (big_m - 37, 2000, 192)]
+    return small, big, cus
+
+
+def test_linear_dense_split_k_and_plain(dev):
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_FP16_FP32OUT, DTYPE_INT8
+    small, big, cus = _dense_shapes()
+    for (M, N, K) in small + big:
+        tiles = -(-M // 128) * -(-N // 128)
+        assert (tiles <= cus) == ((M, N, K) in small)
+        rng = np.random.default_rng(seed_for(4, 80) + M + N + K)
+        A = rng.integers(-127, 128, (M, K)).astype(np.int8)
+        W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+        D = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8, transB=1)
+        torch.cuda.synchronize()
+        ref = A.astype(np.int64) @ W.astype(np.int64).T
+        got = D.cpu().numpy().astype(np.int64)
+        assert np.array_equal(got, ref), (M, N, K, int((got != ref).sum()))
+        Af, Bf = _f16(rng, M, K), _f16(rng, N, K)
+        D = ops.linear(to_dev(Af, dev), to_dev(Bf, dev), M, N, K, DTYPE_FP16_FP32OUT, transB=1)
+        torch.cuda.synchronize()
+        ref = Af.astype(np.float64) @ Bf.astype(np.float64).T
+        assert rel_err(D.cpu().numpy(), ref) <= TOL_F32, (M, N, K)
+
+
+def test_linear_dense_split_k_repeatable(dev):
+    """The split-K kernel adds the two groups' fp32 sums in one fixed order:
+    the same inputs give the same bits on every call."""
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_FP16
+    M, N, K = 512, 1024, 2048
+    rng = np.random.default_rng(seed_for(4, 81))
+    A, B = to_dev(_f16(rng, M, K), dev), to_dev(_f16(rng, N, K), dev)
+    outs = [ops.linear(A, B, M, N, K, DTYPE_FP16, transB=1) for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+
+
 def test_config4_linear_int8(dev):
     """C4: int8 [512,5120] x int8 [5120,5120]^T, per-token and per-channel
     scales, fp16 bias, fp16 out."""

@@ -367,13 +367,12 @@ int vkflame_dispatch_linear(const void *A, const void *B, const void *C, void *D
     g.ldc = (uint64_t)N;
     g.act = (uint32_t)activation;
     g.flags = (transA ? VKF_GF_X_TRANS : 0u) | (transB ? 0u : VKF_GF_Y_TRANS);
-    dim3 grid(cdiv(N, 128), cdiv(M, 128));
     if (dtype == VKF_DTYPE_FP16 || dtype == VKF_DTYPE_FP16_FP32OUT) {
         g.alpha = alpha ? *(const float *)alpha : 1.0f;
         g.beta = beta ? *(const float *)beta : 0.0f;
         if (g.beta != 0.0f && !C) return kInval;
         if (dtype == VKF_DTYPE_FP16_FP32OUT) g.flags |= VKF_GF_D_F32 | VKF_GF_CIN_F32;
-        return vkf::launch(VKF_K_GEMM_F16, grid, dim3(256), g, S(stream));
+        return vkf::launch_gemm(VKF_K_GEMM_F16, g, S(stream));
     }
     if (dtype == VKF_DTYPE_INT8) {
         if (activation != 0) return kInval;
@@ -381,7 +380,7 @@ int vkflame_dispatch_linear(const void *A, const void *B, const void *C, void *D
         g.beta = beta ? (float)*(const int32_t *)beta : 0.0f;
         if (g.beta != 0.0f && !C) return kInval;
         g.flags |= VKF_GF_D_I32;
-        return vkf::launch(VKF_K_GEMM_I8, grid, dim3(256), g, S(stream));
+        return vkf::launch_gemm(VKF_K_GEMM_I8, g, S(stream));
     }
     return kNotSup;  // FP32 and BF16 GEMM are outside this library's path
 }
@@ -411,8 +410,7 @@ int vkflame_dispatch_linear_int8(const int8_t *A, const float *a_scale, const in
     g.alpha = 1.0f;
     g.beta = 0.0f;
     g.flags = (d_dtype == VKF_DTYPE_FP32 ? VKF_GF_D_F32 : 0u) | (bias_dtype == VKF_DTYPE_FP32 ? VKF_GF_BIAS_F32 : 0u);
-    dim3 grid(cdiv(N, 128), cdiv(M, 128));
-    return vkf::launch(VKF_K_GEMM_I8, grid, dim3(256), g, S(stream));
+    return vkf::launch_gemm(VKF_K_GEMM_I8, g, S(stream));
 }
 
 }  // extern "C"

@@ -136,10 +136,24 @@ hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const void *args, size_
                                  params, nullptr);
 }
 
+// The condition under which the dense GEMM kernels take their direct-to-LDS
+// main loop (dma_ok in kernels/gemm.hip): K-contiguous rows, 16-byte aligned
+// base and row pitch, K*es a multiple of 128 bytes.
+static bool dma_operand(const void *p, uint64_t ld, bool trans, uint32_t K, uint32_t es) {
+    return !trans && (ld * es) % 16 == 0 && ((uintptr_t)p & 15) == 0 && ((uint64_t)K * es) % 128 == 0;
+}
+
 hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream) {
     if (g.R == 0 || g.Cn == 0) return hipSuccess;
     dim3 grid((g.Cn + 127) / 128, (g.R + 127) / 128);
     if (grid.y > 65535) return hipErrorInvalidValue;
+    if ((id == VKF_K_GEMM_F16 || id == VKF_K_GEMM_I8) && (uint64_t)grid.x * grid.y <= (uint64_t)cu_count()) {
+        const uint32_t es = id == VKF_K_GEMM_F16 ? 2 : 1;
+        if (dma_operand(g.X, g.ldx, (g.flags & VKF_GF_X_TRANS) != 0, g.K, es) &&
+            dma_operand(g.Y, g.ldy, (g.flags & VKF_GF_Y_TRANS) != 0, g.K, es))
+            return launch(id == VKF_K_GEMM_F16 ? VKF_K_GEMM_F16_K2 : VKF_K_GEMM_I8_K2, grid, dim3(512), &g,
+                          sizeof(g), stream);
+    }
     return launch(id, grid, dim3(256), &g, sizeof(g), stream);
 }
 

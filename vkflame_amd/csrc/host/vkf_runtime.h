@@ -92,6 +92,8 @@
     X(GEMV_DOT_Q5_K_F32_M4, "vkf_gemv_dot_q5_k_f32_m4") \
     X(GEMM_F16, "vkf_gemm_f16")                             \
     X(GEMM_I8, "vkf_gemm_i8")                               \
+    X(GEMM_F16_K2, "vkf_gemm_f16_k2")                       \
+    X(GEMM_I8_K2, "vkf_gemm_i8_k2")                         \
     /* GEMM: fp16 and Q8_1 activations per weight type */   \
     X(GEMM_Q4_0_F16, "vkf_gemm_q4_0_f16")                   \
     X(GEMM_Q4_0_Q81, "vkf_gemm_q4_0_q8_1")                  \
@@ -139,7 +141,9 @@ inline hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const T &args, h
     return launch(id, grid, block, &args, sizeof(T), stream, shmem);
 }
 
-// A VkfGemmArgs launch: 128x128 output tile per 256-thread workgroup.
+// A VkfGemmArgs launch: 128x128 output tile per 256-thread workgroup.  For
+// GEMM_F16 / GEMM_I8 with no more tiles than CUs and operands the
+// direct-to-LDS loads take, the 512-thread split-K kernel (_K2) instead.
 hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream);
 
 // VKFLAME_DEBUG=1: one stderr line per dispatch (reference: torch_backend/mode.py:13).

@@ -1241,3 +1241,136 @@ GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a) {
             }
 }
 
+
+// ---------------------------------------------------------------------------
+// Dense GEMM with the K loop split inside the workgroup, for grids with no
+// more 128 x 128 tiles than the chip has CUs (M = 512 x N = 5120: 160 tiles
+// on 256 CUs).  There the 256-thread kernel runs one workgroup, one wave per
+// SIMD, on each busy CU, and nothing overlaps a wave's LDS fragment reads
+// with its MFMAs.  Here 512 threads hold the same 128 x 128 tile: waves 0-3
+// (group 0) take the even 128-byte K steps, waves 4-7 (group 1) the odd
+// ones, each wave a 64 x 64 quadrant as in the 256-thread kernel, so every
+// SIMD runs two waves.  Both groups' tiles of a step pair arrive by
+// direct-to-LDS loads (two stages of 2 x 32 KiB); at the end group 1's
+// accumulators go through LDS and group 0 adds them, the same order on every
+// run (int32 sums are exact, fp32 ones differ from the sequential K order
+// only in rounding).  Aligned K-contiguous operands with K*ES a multiple of
+// 128 only (the host checks this before it picks these kernels).
+// ---------------------------------------------------------------------------
+#define GEMM_K2_LDS (2 * 65536)
+#define GEMM_KERNEL_K2 VKF_KERNEL void __launch_bounds__(512)
+
+template <int ES, class ACC>
+__device__ __forceinline__ void gemm_mainloop_dma_k2(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, ACC acc[4][4],
+                                                     uint8_t *smem) {
+    const int wave = threadIdx.x >> 6, g = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
+    const int wr = wq >> 1, wc = wq & 1;
+    const uint32_t nk = (uint32_t)(((uint64_t)a.K * ES) / 128);
+    const uint8_t *gx[4], *gy[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t rr = (4 * wq + j) * 8 + (lane >> 3);
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t rx = r0 + rr < a.R ? r0 + rr : a.R - 1;  // rows past the edge: any valid row
+        const uint32_t ry = c0 + rr < a.Cn ? c0 + rr : a.Cn - 1;
+        gx[j] = (const uint8_t *)a.X + (uint64_t)rx * a.ldx * ES + ch * 16;
+        gy[j] = (const uint8_t *)a.Y + (uint64_t)ry * a.ldy * ES + ch * 16;
+    }
+    // step kt of this group into its half of stage st
+    auto issue = [&](uint32_t kt, uint32_t st) {
+        uint8_t *sx = smem + st * 65536 + g * 32768, *sy = sx + 16384;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t off = (4 * wq + j) * 8 * 128;
+            vkf_load_lds16(gx[j] + (uint64_t)kt * 128, sx + off);
+            vkf_load_lds16(gy[j] + (uint64_t)kt * 128, sy + off);
+        }
+    };
+    const uint32_t npair = (nk + 1) / 2;
+    if ((uint32_t)g < nk) issue(g, 0);
+    for (uint32_t t = 0; t < npair; t++) {
+        wait_vm<0>();  // this thread's loads of pair t are the only ones in flight
+        __syncthreads();
+        const uint32_t kn = 2 * (t + 1) + g;
+        if (kn < nk) issue(kn, (t + 1) & 1);
+        if (2 * t + g < nk) {
+            const uint8_t *lx = smem + (t & 1) * 65536 + g * 32768;
+            mfma_step_swz<ES>(lx, lx + 16384, wr, wc, acc);
+        }
+    }
+    __syncthreads();  // LDS free for the reduction
+    // group 1's accumulators -> LDS (lane-major, 64 KiB), group 0 adds them
+    vkf_i4 *red = (vkf_i4 *)smem;
+    if (g == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) red[(wq * 16 + 4 * i + j) * 64 + lane] = __builtin_bit_cast(vkf_i4, acc[i][j]);
+    }
+    __syncthreads();
+    if (g == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] += __builtin_bit_cast(ACC, red[(wq * 16 + 4 * i + j) * 64 + lane]);
+    }
+    __syncthreads();  // LDS free for the epilogue
+}
+
+// epilogue of the split-K kernels: group 0 stages the tile, all 512 threads store it
+template <class ACC>
+__device__ __forceinline__ void epilogue_tile_k2(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC acc[4][4],
+                                                 uint8_t *smem) {
+    const int wave = threadIdx.x >> 6;
+    if (wave < 4) epi_stage(a, r0, c0, acc, (float *)smem, (wave & 3) >> 1, wave & 1);
+    __syncthreads();
+    epi_store<512>(a, r0, c0, (const float *)smem);
+}
+
+GEMM_KERNEL_K2 vkf_gemm_f16_k2(VkfGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_K2_LDS];
+    uint32_t r0, c0;
+    gemm_tile_of(r0, c0);
+    vkf_f4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
+    gemm_mainloop_dma_k2<2>(a, r0, c0, acc, smem);
+    epilogue_tile_k2(a, r0, c0, acc, smem);
+}
+
+GEMM_KERNEL_K2 vkf_gemm_i8_k2(VkfGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_K2_LDS];
+    uint32_t r0, c0;
+    gemm_tile_of(r0, c0);
+    vkf_i4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = vkf_i4{0, 0, 0, 0};
+    gemm_mainloop_dma_k2<1>(a, r0, c0, acc, smem);
+    if (!(a.flags & VKF_GF_D_I32)) {
+        epilogue_tile_k2(a, r0, c0, acc, smem);
+        return;
+    }
+    if (threadIdx.x >= 256) return;  // group 0 holds the sums; no barrier follows
+    // raw int32 accumulator with integer alpha/beta (hipblasGemmEx, compute 32I)
+    const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
+    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+    const int32_t al = (int32_t)a.alpha, be = (int32_t)a.beta;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t r = r0 + wr * 64 + 16 * i + 4 * lg + e, c = c0 + wc * 64 + 16 * j + li;
+                if (r < a.R && c < a.Cn) {
+                    int32_t v = acc[i][j][e];
+                    if (al != 1 || be != 0)
+                        v = al * v + (be ? be * ((const int32_t *)a.Cin)[(uint64_t)r * a.ldc + c] : 0);
+                    ((int32_t *)a.D)[(uint64_t)r * a.ldd + c] = v;
+                }
+            }
+}
