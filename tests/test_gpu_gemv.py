@@ -222,6 +222,36 @@ def test_gemv_mfma(dev, qt, M, N, K):
     assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32
 
 
+@pytest.mark.parametrize("M", [2, 5, 8, 9, 16])
+@pytest.mark.parametrize("N", [77, 3001])
+@pytest.mark.parametrize("K", [2560, 13824])
+def test_gemv_mfma_q6_k(dev, M, N, K):
+    """Q6_K x fp16 at 2 <= M <= 16 on the matrix cores: 210-byte super-blocks
+    at alternating 2-byte alignment (every odd one), K = 13824 as two K-slice
+    launches of 27 super-blocks (the second slice starting 2 bytes into a
+    dword).  The operand sc*(q-32) is rounded to fp16 above 2048."""
+    from vkflame_amd import ops
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(2, 90 + M))
+    xa, x64 = _x("f16", M, K, seed_for(2, 95 + M))
+    y = ops.gemm_q(to_dev(w, dev), O.Q6_K, to_dev(xa, dev), N, K).cpu().numpy()
+    assert _per_row_err(y, x64, w, O.Q6_K, N, K) <= TOL_F32
+
+
+def test_gemv_mfma_q6_k_extreme_scales(dev):
+    """Every scale at -128 or 127 and codes at 0 / 63: operands of magnitude
+    up to 4096, the fp16 rounding at its largest."""
+    from vkflame_amd import ops
+    N, K, M = 300, 4096, 8
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(2, 97)).reshape(N, K // 256, 210).copy()
+    rng = np.random.default_rng(seed_for(2, 98))
+    w[:, :, 192:208] = rng.choice(np.array([0x80, 0x7F], dtype=np.uint8), size=(N, K // 256, 16))
+    w[:, :, 0:192] = rng.choice(np.array([0x00, 0xFF], dtype=np.uint8), size=(N, K // 256, 192))
+    w = w.reshape(N, -1)
+    xa, x64 = _x("f16", M, K, seed_for(2, 99))
+    y = ops.gemm_q(to_dev(w, dev), O.Q6_K, to_dev(xa, dev), N, K).cpu().numpy()
+    assert _per_row_err(y, x64, w, O.Q6_K, N, K) <= TOL_F32
+
+
 @pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_1, O.Q4_K, O.Q5_K], ids=["q4_0", "q4_1", "q4_k", "q5_k"])
 @pytest.mark.parametrize("kind", ["f16", "f32"])
 @pytest.mark.parametrize("NK", [(77, 1600), (77, 1664), (77, 1728), (3001, 4096), (100003, 2624)],

@@ -1,5 +1,5 @@
-// gemv_mfma.hip — small-batch GEMV (2 <= M <= 16) of Q4_K, Q4_0 and Q4_1
-// weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T, fp16
+// gemv_mfma.hip — small-batch GEMV (2 <= M <= 16) of Q4_K, Q4_0, Q4_1 and
+// Q6_K weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T, fp16
 // activations.
 //
 // With 2..16 activation rows the VALU dot product costs M multiply-adds per
@@ -18,6 +18,12 @@
 // in fp32; dall is applied once per super-block.  The min term is one more
 // MFMA whose k runs over the 8 sub-blocks: A = xs/32 as two fp16 halves
 // (hi + lo, ~22 bits) on k-slices 0 and 1, B = mn.
+//
+// Q6_K arithmetic.  A weight is d*sc*(q - 32) (kernels/dequant_q6_k.glsl;
+// sc int8 per 16 elements, q 6 bits from a ql nibble and two qh bits).  The
+// MFMA operand is sc*(q - 32) in fp16: an integer of magnitude <= 4096,
+// exact up to 2048 and rounded once (relative 2^-12) above; d is applied
+// once per super-block to the fp32 sum of its 8 MFMAs.
 //
 // Q4_0 / Q4_1 arithmetic.  The MFMA operand is the dequantised weight in
 // fp16, d*(q-8) (kernels/dequant_q4_0.glsl) or d*q + m (dequant_q4_1.glsl),
@@ -38,6 +44,13 @@
 //   elements 16(g&1) .. +15 of sub-blocks j = 4L + 2(g>>1) + nib (L = which
 //   load, nib = low / high nibbles).  Step t = 4L + 2nib + hf takes, in
 //   k-slice g, elements 16(g&1) + 8hf .. +7 of that sub-block.
+//   Q6_K: ql bytes 16g .. +15 and 64 + 16g .. +15 (halves n = 0, 1), qh
+//   bytes 128 + 16(g&1) .. and 160 + 16(g&1) .., the 16 scales, d.  Element
+//   x of ql byte run n is k = 128n + 64h + 16g + x for nibble h, its two high
+//   bits at 4h + 2(g>>1) of qh byte 32n + 16(g&1) + x, its scale byte
+//   8n + 4h + g.  Step t = 4n + 2h + hf takes elements x = 8hf .. +7.  Super-
+//   blocks (210 bytes) are 2-byte aligned: each run loads from the 4-byte
+//   aligned address below it and is shifted into place (v_alignbyte).
 //   Q4_0 / Q4_1: the block pair 2g, 2g+1 of the group (36 or 40 contiguous
 //   bytes, 4-byte aligned).  Step t = 4blk + 2nib + hf takes, in k-slice g,
 //   elements 16nib + 8hf .. +7 of block 2g + blk (low nibbles of qs bytes
@@ -55,12 +68,12 @@
 #include "vkf_device.h"
 
 #define GM_WAVES 16
-enum { GF_Q4_K = 0, GF_Q4_0 = 1, GF_Q4_1 = 2 };
+enum { GF_Q4_K = 0, GF_Q4_0 = 1, GF_Q4_1 = 2, GF_Q6_K = 3 };
 
 // 256-k groups per wave held in registers at once (the most without spills)
-template <int F> constexpr int gm_maxsb() { return F == GF_Q4_K ? 5 : 4; }
+template <int F> constexpr int gm_maxsb() { return F == GF_Q4_K ? 5 : F == GF_Q6_K ? 1 : 4; }
 
-template <int F> constexpr uint32_t gm_group_bytes() { return F == GF_Q4_1 ? 160 : 144; }
+template <int F> constexpr uint32_t gm_group_bytes() { return F == GF_Q4_1 ? 160 : F == GF_Q6_K ? 210 : 144; }
 
 // k offset, within its 256-k group, of the 8 elements of MFMA step t, k-slice g
 template <int F>
@@ -68,6 +81,8 @@ __device__ __forceinline__ uint32_t gm_k0(uint32_t t, uint32_t g) {
     if constexpr (F == GF_Q4_K) {
         const uint32_t j = 4 * (t >> 2) + 2 * (g >> 1) + ((t >> 1) & 1), r = 2 * (g & 1) + (t & 1);
         return 32 * j + 8 * r;
+    } else if constexpr (F == GF_Q6_K) {
+        return 128 * (t >> 2) + 64 * ((t >> 1) & 1) + 16 * g + 8 * (t & 1);
     } else {
         return 64 * g + 32 * (t >> 2) + 16 * ((t >> 1) & 1) + 8 * (t & 1);
     }
@@ -149,17 +164,40 @@ __device__ __forceinline__ void gm_stage_pass(const VkfGemvArgs &a, unsigned cha
 
 // One lane's share of a 256-k group: Q4_K header, qs 16g.. and 64+16g..;
 // Q4_0 the 36 bytes of block pair g (v[2][0] last); Q4_1 its 40 bytes
-// (v[2][0..1] last).
+// (v[2][0..1] last); Q6_K its four 16-byte runs and the scales, each as the
+// 20 bytes from the 4-byte aligned address below it, and d.
+template <int F>
 struct GmSb {
     vkf_u4 v[3];
 };
+template <>
+struct GmSb<GF_Q6_K> {
+    vkf_u4 r[5];     // ql run 0, ql run 1, qh run 0, qh run 1, scales: first 16 bytes
+    uint32_t e[5];   // the dword after each
+    uint32_t d, sh;  // d (fp16 bits); byte offset of the super-block in its dword
+};
 
 template <int F>
-__device__ __forceinline__ void gm_load(const uint8_t *row, uint32_t sb, int g, GmSb &t) {
+__device__ __forceinline__ void gm_load(const uint8_t *row, uint32_t sb, int g, GmSb<F> &t) {
     typedef unsigned int u4a4 __attribute__((ext_vector_type(4), aligned(4)));
     typedef unsigned int u2a4 __attribute__((ext_vector_type(2), aligned(4)));
     const uint8_t *b = row + (uint64_t)gm_group_bytes<F>() * sb;
-    if constexpr (F == GF_Q4_K) {
+    if constexpr (F == GF_Q6_K) {
+        // runs at 16g, 64 + 16g, 128 + 16(g&1), 160 + 16(g&1), 192; with
+        // sh = 2 the aligned 20 bytes start 2 bytes before the run and end
+        // at its byte 17, for the scales at byte 209 of the super-block (d);
+        // with sh = 0 the scales' extra dword is re-read from byte 204 (not
+        // used) so that no load passes byte 209
+        t.sh = (uint32_t)(uintptr_t)b & 3u;
+        const uint8_t *a = b - t.sh;
+        const uint32_t off[5] = {16u * g, 64u + 16u * g, 128u + 16u * (g & 1), 160u + 16u * (g & 1), 192u};
+#pragma unroll
+        for (int k = 0; k < 5; k++) {
+            t.r[k] = *(const u4a4 *)(a + off[k]);
+            t.e[k] = *(const uint32_t *)(a + off[k] + (k < 4 || t.sh ? 16 : 12));
+        }
+        t.d = *(const uint16_t *)(b + 208);
+    } else if constexpr (F == GF_Q4_K) {
         t.v[0] = *(const vkf_u4 *)b;
         t.v[1] = *(const vkf_u4 *)(b + 16 + 16 * g);
         t.v[2] = *(const vkf_u4 *)(b + 80 + 16 * g);
@@ -182,13 +220,13 @@ __device__ __forceinline__ void gm_load(const uint8_t *row, uint32_t sb, int g, 
 // sb1 - 1 (loaded and not used), so that the loads form one straight
 // sequence.  sb1 >= 1.
 template <int F>
-__device__ __forceinline__ void gm_load_batch(const uint8_t *row, uint32_t s0, uint32_t sb1, int g, GmSb *t) {
+__device__ __forceinline__ void gm_load_batch(const uint8_t *row, uint32_t s0, uint32_t sb1, int g, GmSb<F> *t) {
 #pragma unroll
     for (int u = 0; u < gm_maxsb<F>(); u++) gm_load<F>(row, s0 + u < sb1 ? s0 + u : sb1 - 1, g, t[u]);
 }
 
 // load instructions gm_load issues
-template <int F> constexpr int gm_loads_per_group() { return 3; }
+template <int F> constexpr int gm_loads_per_group() { return F == GF_Q6_K ? 11 : 3; }
 
 __device__ __forceinline__ vkf_h2 gm_h2(uint32_t u) { return __builtin_bit_cast(vkf_h2, u); }
 __device__ __forceinline__ uint32_t gm_u(vkf_h2 h) { return __builtin_bit_cast(uint32_t, h); }
@@ -248,6 +286,25 @@ __device__ __forceinline__ vkf_h8 gm_decode_w(uint32_t d0, uint32_t d1, _Float16
 
 __device__ __forceinline__ _Float16 gm_f16(uint32_t bits) { return __builtin_bit_cast(_Float16, (uint16_t)bits); }
 
+// Q6_K: sc*(q - 32) of 8 elements from ql dwords d0, d1 (nibble HI) and qh
+// dwords e0, e1 (two bits at qs of each byte); sc2 = {sc, sc}
+template <int HI>
+__device__ __forceinline__ vkf_h8 gm_decode_q6(uint32_t d0, uint32_t d1, uint32_t e0, uint32_t e1, uint32_t qs,
+                                               vkf_h2 sc2, uint32_t c64) {
+    const vkf_h2 m1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+    const uint32_t n0 = HI ? d0 >> 4 : d0, n1 = HI ? d1 >> 4 : d1;
+    const uint32_t b0 = ((e0 >> qs) & 0x03030303u) << 4, b1 = ((e1 >> qs) & 0x03030303u) << 4;
+    // (1024 + q) pairs (bytes 0,2 then 1,3 of each dword)
+    const uint32_t p[4] = {gm_and_or(b0, 0x00300030u, gm_and_or(n0, 0x000f000fu, c64)),
+                           gm_and_or(b0 >> 8, 0x00300030u, gm_and_or(n0 >> 8, 0x000f000fu, c64)),
+                           gm_and_or(b1, 0x00300030u, gm_and_or(n1, 0x000f000fu, c64)),
+                           gm_and_or(b1 >> 8, 0x00300030u, gm_and_or(n1 >> 8, 0x000f000fu, c64))};
+    vkf_u4 r;
+#pragma unroll
+    for (int k = 0; k < 4; k++) r[k] = gm_u((gm_h2(p[k]) + m1056) * sc2);
+    return __builtin_bit_cast(vkf_h8, r);
+}
+
 template <int F, uint32_t MR>
 __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *smem) {
     const uint32_t nsb = a.K / 256;
@@ -266,7 +323,7 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
     // in flight.  blockIdx.x * G < ntiles: the host launches at most
     // ceil(ntiles / G) workgroups.
     constexpr int MAXSB = gm_maxsb<F>();
-    GmSb t[MAXSB];
+    GmSb<F> t[MAXSB];
     const uint32_t nc = MR * a.K * 2 / 1024;  // 1 KiB loads of x (MR * K * 2 is a multiple of 4096)
     for (uint32_t c = wave; c < nc; c += GM_WAVES) gm_dma_x<F, MR>(a, smem, c, lane);
     asm volatile("" ::: "memory");
@@ -305,7 +362,38 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
                 const uint32_t sb = s0 + u;
                 if (sb >= sb1) break;
                 const unsigned char *xg = xw + sb * (32 * MR * 16);  // step 8sb
-                if constexpr (F == GF_Q4_K) {
+                if constexpr (F == GF_Q6_K) {
+                    const GmSb<F> &T = t[u];
+                    uint32_t w[5][4];  // the runs, shifted into place
+#pragma unroll
+                    for (int k = 0; k < 5; k++)
+#pragma unroll
+                        for (int c = 0; c < 4; c++)
+                            w[k][c] = __builtin_amdgcn_alignbyte(c < 3 ? T.r[k][c + 1] : T.e[k], T.r[k][c], T.sh);
+                    const uint32_t qs = 2u * (lg >> 1);  // + 4h
+                    vkf_f4 acc = zero;
+#pragma unroll
+                    for (int n = 0; n < 2; n++)
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            const int8_t scb = (int8_t)(w[4][2 * n + h] >> (8 * lg));
+                            const _Float16 sc = (_Float16)(float)scb;
+                            const vkf_h2 sc2 = {sc, sc};
+#pragma unroll
+                            for (int hf = 0; hf < 2; hf++) {
+                                const unsigned char *xp = xg + (4 * n + 2 * h + hf) * (4 * MR * 16);
+                                const vkf_h8 xv = *(const vkf_h8 *)xp;
+                                const uint32_t d0 = w[n][2 * hf], d1 = w[n][2 * hf + 1];
+                                const uint32_t e0 = w[2 + n][2 * hf], e1 = w[2 + n][2 * hf + 1];
+                                const vkf_h8 bv = h ? gm_decode_q6<1>(d0, d1, e0, e1, qs + 4, sc2, c64)
+                                                    : gm_decode_q6<0>(d0, d1, e0, e1, qs, sc2, c64);
+                                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, bv, acc, 0, 0, 0);
+                            }
+                        }
+                    const float d = vkf_h2f(T.d);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) y4[e] = fmaf(d, acc[e], y4[e]);
+                } else if constexpr (F == GF_Q4_K) {
                     const vkf_u4 hdr = t[u].v[0];
                     const float dall = vkf_h2f(hdr[0] & 0xffffu), dmin = vkf_h2f(hdr[0] >> 16);
                     const uint32_t s0w = hdr[1], s4w = hdr[2], s8w = hdr[3];
@@ -422,3 +510,4 @@ __device__ __forceinline__ void gemv_mfma_entry(const VkfGemvArgs &a) {
 VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_k_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_K>(a); }
 VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_0_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_0>(a); }
 VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_1_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_1>(a); }
+VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q6_k_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q6_K>(a); }
