@@ -1,5 +1,5 @@
-// gemv_mfma.hip — small-batch GEMV (2 <= M <= 16) of Q4_K, Q4_0, Q4_1 and
-// Q6_K weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T, fp16
+// gemv_mfma.hip — small-batch GEMV (2 <= M <= 16) of Q4_K, Q5_K, Q4_0, Q4_1
+// and Q6_K weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T, fp16
 // activations.
 //
 // With 2..16 activation rows the VALU dot product costs M multiply-adds per
@@ -18,6 +18,11 @@
 // in fp32; dall is applied once per super-block.  The min term is one more
 // MFMA whose k runs over the 8 sub-blocks: A = xs/32 as two fp16 halves
 // (hi + lo, ~22 bits) on k-slices 0 and 1, B = mn.
+//
+// Q5_K arithmetic: as Q4_K with q = nibble + 16 * (bit j of qh[e]) for
+// element e of sub-block j (kernels/dequant_q5_k.glsl); sc*q <= 63*31 = 1953
+// is still an exact fp16 integer.  The fifth bit goes into the fp16 pair at
+// bit 4 (1024 + q) or bit 8 (1024 + 16q) by one more v_and_or_b32.
 //
 // Q6_K arithmetic.  A weight is d*sc*(q - 32) (kernels/dequant_q6_k.glsl;
 // sc int8 per 16 elements, q 6 bits from a ql nibble and two qh bits).  The
@@ -44,6 +49,8 @@
 //   elements 16(g&1) .. +15 of sub-blocks j = 4L + 2(g>>1) + nib (L = which
 //   load, nib = low / high nibbles).  Step t = 4L + 2nib + hf takes, in
 //   k-slice g, elements 16(g&1) + 8hf .. +7 of that sub-block.
+//   Q5_K: as Q4_K (header; qs bytes 48 + 16g .., 112 + 16g ..) plus qh bytes
+//   16 + 16(g&1) .. +15, the fifth bits of the same elements.
 //   Q6_K: ql bytes 16g .. +15 and 64 + 16g .. +15 (halves n = 0, 1), qh
 //   bytes 128 + 16(g&1) .. and 160 + 16(g&1) .., the 16 scales, d.  Element
 //   x of ql byte run n is k = 128n + 64h + 16g + x for nibble h, its two high
@@ -68,17 +75,22 @@
 #include "vkf_device.h"
 
 #define GM_WAVES 16
-enum { GF_Q4_K = 0, GF_Q4_0 = 1, GF_Q4_1 = 2, GF_Q6_K = 3 };
+enum { GF_Q4_K = 0, GF_Q4_0 = 1, GF_Q4_1 = 2, GF_Q6_K = 3, GF_Q5_K = 4 };
+
+// formats with a per-sub-block min term (dmin * mn), fed by the sub-block sums of x
+template <int F> constexpr bool gm_kmin() { return F == GF_Q4_K || F == GF_Q5_K; }
 
 // 256-k groups per wave held in registers at once (the most without spills)
-template <int F> constexpr int gm_maxsb() { return F == GF_Q4_K ? 5 : F == GF_Q6_K ? 1 : 4; }
+template <int F> constexpr int gm_maxsb() { return F == GF_Q4_K ? 5 : F == GF_Q6_K ? 1 : F == GF_Q5_K ? 3 : 4; }
 
-template <int F> constexpr uint32_t gm_group_bytes() { return F == GF_Q4_1 ? 160 : F == GF_Q6_K ? 210 : 144; }
+template <int F> constexpr uint32_t gm_group_bytes() {
+    return F == GF_Q4_1 ? 160 : F == GF_Q6_K ? 210 : F == GF_Q5_K ? 176 : 144;
+}
 
 // k offset, within its 256-k group, of the 8 elements of MFMA step t, k-slice g
 template <int F>
 __device__ __forceinline__ uint32_t gm_k0(uint32_t t, uint32_t g) {
-    if constexpr (F == GF_Q4_K) {
+    if constexpr (gm_kmin<F>()) {
         const uint32_t j = 4 * (t >> 2) + 2 * (g >> 1) + ((t >> 1) & 1), r = 2 * (g & 1) + (t & 1);
         return 32 * j + 8 * r;
     } else if constexpr (F == GF_Q6_K) {
@@ -100,7 +112,7 @@ __device__ __forceinline__ uint32_t gm_k0(uint32_t t, uint32_t g) {
 // Staging: direct-to-LDS loads put each 16-byte piece of x in place (piece
 // = lane of a 1 KiB load), then a pass reorders the halves of every piece
 // (and, for Q4_K, writes the sub-block sums).
-template <int F> constexpr uint32_t gm_xs_bytes_per_group(uint32_t MR) { return F == GF_Q4_K ? 32 * MR : 0; }
+template <int F> constexpr uint32_t gm_xs_bytes_per_group(uint32_t MR) { return gm_kmin<F>() ? 32 * MR : 0; }
 
 // the x pieces of the workgroup's 1 KiB direct load c
 template <int F, uint32_t MR>
@@ -120,7 +132,7 @@ __device__ __forceinline__ vkf_u4 gm_reorder(vkf_u4 v) {
 // the reorder (and Q4_K's sub-block sums), after the direct loads have landed
 template <int F, uint32_t MR>
 __device__ __forceinline__ void gm_stage_pass(const VkfGemvArgs &a, unsigned char *lds) {
-    if constexpr (F != GF_Q4_K) {
+    if constexpr (!gm_kmin<F>()) {
         const uint32_t pieces = (a.K / 8) * MR;
         for (uint32_t p = threadIdx.x; p < pieces; p += blockDim.x) {
             vkf_u4 *pc = (vkf_u4 *)(lds + p * 16);
@@ -171,6 +183,10 @@ struct GmSb {
     vkf_u4 v[3];
 };
 template <>
+struct GmSb<GF_Q5_K> {
+    vkf_u4 v[4];  // header, qh run, qs runs
+};
+template <>
 struct GmSb<GF_Q6_K> {
     vkf_u4 r[5];     // ql run 0, ql run 1, qh run 0, qh run 1, scales: first 16 bytes
     uint32_t e[5];   // the dword after each
@@ -197,6 +213,11 @@ __device__ __forceinline__ void gm_load(const uint8_t *row, uint32_t sb, int g, 
             t.e[k] = *(const uint32_t *)(a + off[k] + (k < 4 || t.sh ? 16 : 12));
         }
         t.d = *(const uint16_t *)(b + 208);
+    } else if constexpr (F == GF_Q5_K) {
+        t.v[0] = *(const vkf_u4 *)b;
+        t.v[1] = *(const vkf_u4 *)(b + 16 + 16 * (g & 1));
+        t.v[2] = *(const vkf_u4 *)(b + 48 + 16 * g);
+        t.v[3] = *(const vkf_u4 *)(b + 112 + 16 * g);
     } else if constexpr (F == GF_Q4_K) {
         t.v[0] = *(const vkf_u4 *)b;
         t.v[1] = *(const vkf_u4 *)(b + 16 + 16 * g);
@@ -226,7 +247,7 @@ __device__ __forceinline__ void gm_load_batch(const uint8_t *row, uint32_t s0, u
 }
 
 // load instructions gm_load issues
-template <int F> constexpr int gm_loads_per_group() { return F == GF_Q6_K ? 11 : 3; }
+template <int F> constexpr int gm_loads_per_group() { return F == GF_Q6_K ? 11 : F == GF_Q5_K ? 4 : 3; }
 
 __device__ __forceinline__ vkf_h2 gm_h2(uint32_t u) { return __builtin_bit_cast(vkf_h2, u); }
 __device__ __forceinline__ uint32_t gm_u(vkf_h2 h) { return __builtin_bit_cast(uint32_t, h); }
@@ -262,6 +283,23 @@ __device__ __forceinline__ vkf_h8 gm_decode(uint32_t d0, uint32_t t0, uint32_t d
     vkf_u4 r;
 #pragma unroll
     for (int p = 0; p < 4; p++) r[p] = gm_u(__builtin_elementwise_fma(h[p], s2, n2));
+    return __builtin_bit_cast(vkf_h8, r);
+}
+
+// Q5_K: gm_decode with the fifth bits; u0, u1 = the qh dwords of d0, d1
+// shifted right by the sub-block index, so bit 0 of each byte is the bit
+template <int HI>
+__device__ __forceinline__ vkf_h8 gm_decode5(uint32_t d0, uint32_t t0, uint32_t d1, uint32_t t1, uint32_t u0,
+                                             uint32_t u1, _Float16 s, _Float16 n, uint32_t c64) {
+    vkf_h2 h[4];
+    gm_nibbles<HI>(d0, t0, d1, t1, c64, h);
+    const uint32_t m5 = HI ? 0x01000100u : 0x00100010u;
+    const uint32_t f[4] = {HI ? u0 << 8 : u0 << 4, HI ? u0 : u0 >> 4, HI ? u1 << 8 : u1 << 4, HI ? u1 : u1 >> 4};
+    const vkf_h2 s2 = {s, s}, n2 = {n, n};
+    vkf_u4 r;
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+        r[p] = gm_u(__builtin_elementwise_fma(gm_h2(gm_and_or(f[p], m5, gm_u(h[p]))), s2, n2));
     return __builtin_bit_cast(vkf_h8, r);
 }
 
@@ -393,7 +431,7 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
                     const float d = vkf_h2f(T.d);
 #pragma unroll
                     for (int e = 0; e < 4; e++) y4[e] = fmaf(d, acc[e], y4[e]);
-                } else if constexpr (F == GF_Q4_K) {
+                } else if constexpr (gm_kmin<F>()) {
                     const vkf_u4 hdr = t[u].v[0];
                     const float dall = vkf_h2f(hdr[0] & 0xffffu), dmin = vkf_h2f(hdr[0] >> 16);
                     const uint32_t s0w = hdr[1], s4w = hdr[2], s8w = hdr[3];
@@ -417,14 +455,24 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
                     for (int L = 0; L < 2; L++)
 #pragma unroll
                         for (int hf = 0; hf < 2; hf++) {
-                            const vkf_u4 q = t[u].v[1 + L];
+                            const vkf_u4 q = t[u].v[(F == GF_Q5_K ? 2 : 1) + L];
                             const uint32_t d0 = q[2 * hf], d1 = q[2 * hf + 1], e0 = d0 >> 8, e1 = d1 >> 8;
                             // MFMA steps 8sb + 4L + hf (low nibbles) and 8sb + 4L + 2 + hf (high)
                             const unsigned char *xp = xg + (4 * L + hf) * (4 * MR * 16);
                             const vkf_h8 xl = *(const vkf_h8 *)xp;
                             const vkf_h8 xh = *(const vkf_h8 *)(xp + 2 * (4 * MR * 16));
-                            const vkf_h8 bl = gm_decode<0>(d0, e0, d1, e1, S[L][0], Nn[L][0], c64);
-                            const vkf_h8 bh = gm_decode<1>(d0, e0, d1, e1, S[L][1], Nn[L][1], c64);
+                            vkf_h8 bl, bh;
+                            if constexpr (F == GF_Q5_K) {
+                                // sub-blocks 4L + 2(g>>1) (low nibbles) and + 1 (high)
+                                const uint32_t jl = 4 * L + 2 * (lg >> 1);
+                                const uint32_t h0 = t[u].v[1][2 * hf], h1 = t[u].v[1][2 * hf + 1];
+                                bl = gm_decode5<0>(d0, e0, d1, e1, h0 >> jl, h1 >> jl, S[L][0], Nn[L][0], c64);
+                                bh = gm_decode5<1>(d0, e0, d1, e1, h0 >> (jl + 1), h1 >> (jl + 1), S[L][1], Nn[L][1],
+                                                   c64);
+                            } else {
+                                bl = gm_decode<0>(d0, e0, d1, e1, S[L][0], Nn[L][0], c64);
+                                bh = gm_decode<1>(d0, e0, d1, e1, S[L][1], Nn[L][1], c64);
+                            }
                             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, acc, 0, 0, 0);
                             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, acc, 0, 0, 0);
                         }
@@ -511,3 +559,4 @@ VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_k_f16(VkfGemvA
 VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_0_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_0>(a); }
 VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_1_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_1>(a); }
 VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q6_k_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q6_K>(a); }
+VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q5_k_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q5_K>(a); }
