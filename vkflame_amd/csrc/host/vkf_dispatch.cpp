@@ -214,7 +214,7 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
         if (xk == 1 && (!aligned(x, 16) || (ldx % 4) != 0)) return kInval;
         VkfGemvArgs a{(const uint8_t *)w, x, y, row_bytes, (uint64_t)ldx, (uint64_t)ldy,
                       (uint32_t)M, (uint32_t)N, (uint32_t)K, 0u};
-        // Q4_K, Q4_0, Q4_1, Q6_K, Q5_K x fp16 at 2 <= M <= 16 on the matrix cores
+        // Q4_K, Q4_0, Q4_1, Q6_K, Q5_K, Q8_0 x fp16 at 2 <= M <= 16 on the matrix cores
         // (kernels/gemv_mfma.hip; faster than the dot GEMV from M = 2 up,
         // e.g. Q4_0 11008x4096 M=4 13.2 vs 16.9 us on MI355X): the
         // activations of a K slice staged for 8 or 16 rows (512 bytes per
@@ -226,18 +226,23 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
                        : qt == VKF_Q4_1 ? 2
                        : qt == VKF_Q6_K ? 3
                        : qt == VKF_Q5_K ? 4
+                       : qt == VKF_Q8_0 ? 5
                                         : -1;
         const bool kmin = mf == 0 || mf == 4;  // Q4_K / Q5_K: sub-block sums of x staged too
+        // Q8_0 at M <= 4 stays on the dot GEMV unless N gives two tiles per CU
+        // (4096x4096 M=4: 11.6 us there against 13.2 here; 13824x5120 M=4:
+        // 25.5 against 21.9)
+        const bool mf_ok = mf != 5 || M > 4 || cdiv(N, 16) >= 2u * (uint32_t)vkf::cu_count();
         const uint32_t mr = M <= 8 ? 8 : 16, ga = kmin ? 16 : 4;
         const size_t per_group = (size_t)mr * (kmin ? 544 : 512);
-        if (mf >= 0 && M >= 2 && xk == 0 && (K % 256) == 0 && aligned(w, ga) && (row_bytes % ga) == 0 &&
+        if (mf >= 0 && mf_ok && M >= 2 && xk == 0 && (K % 256) == 0 && aligned(w, ga) && (row_bytes % ga) == 0 &&
             vkf::max_lds() >= kMfmaRed + per_group) {
             const uint32_t nsb = (uint32_t)(K / 256), cap = (uint32_t)((vkf::max_lds() - kMfmaRed) / per_group);
             const uint32_t slices = cdiv(nsb, cap), per = cdiv(nsb, slices);
             const uint32_t cus = (uint32_t)vkf::cu_count(), tiles = cdiv(N, 16);
             const uint32_t P = mfma_split(tiles, cus);
             const uint32_t G = 16 / P, grid = cdiv(tiles, G) < cus ? cdiv(tiles, G) : cus;
-            const uint64_t group_bytes = mf == 2 ? 160 : mf == 3 ? 210 : mf == 4 ? 176 : 144;
+            const uint64_t group_bytes = mf == 2 ? 160 : mf == 3 ? 210 : mf == 4 ? 176 : mf == 5 ? 272 : 144;
             const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_MFMA_Q4_K_F16 + mf);
             for (uint32_t s0 = 0; s0 < nsb; s0 += per) {
                 const uint32_t n_sb = nsb - s0 < per ? nsb - s0 : per;

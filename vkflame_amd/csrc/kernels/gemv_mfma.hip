@@ -1,5 +1,5 @@
-// gemv_mfma.hip — small-batch GEMV (2 <= M <= 16) of Q4_K, Q5_K, Q4_0, Q4_1
-// and Q6_K weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T, fp16
+// gemv_mfma.hip — small-batch GEMV (2 <= M <= 16) of Q4_K, Q5_K, Q4_0, Q4_1,
+// Q8_0 and Q6_K weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T, fp16
 // activations.
 //
 // With 2..16 activation rows the VALU dot product costs M multiply-adds per
@@ -30,9 +30,11 @@
 // exact up to 2048 and rounded once (relative 2^-12) above; d is applied
 // once per super-block to the fp32 sum of its 8 MFMAs.
 //
-// Q4_0 / Q4_1 arithmetic.  The MFMA operand is the dequantised weight in
-// fp16, d*(q-8) (kernels/dequant_q4_0.glsl) or d*q + m (dequant_q4_1.glsl),
-// rounded once from the exact value; products and sums run in fp32.
+// Q4_0 / Q4_1 / Q8_0 arithmetic.  The MFMA operand is the dequantised weight
+// in fp16, d*(q-8) (kernels/dequant_q4_0.glsl), d*q + m (dequant_q4_1.glsl)
+// or d*q (dequant_q8_0.glsl), rounded once from the exact value; products
+// and sums run in fp32.  Q8_0 codes become fp16 pairs as
+// (1024 + (b ^ 0x80)) - 1152 = b.
 //
 // Decode.  A code dword holds bytes b0..b3.  (v & 0x000f000f) | 0x64006400 is
 // the fp16 pair (1024 + b0.lo, 1024 + b2.lo); mask 0x00f000f0 gives
@@ -58,6 +60,8 @@
 //   8n + 4h + g.  Step t = 4n + 2h + hf takes elements x = 8hf .. +7.  Super-
 //   blocks (210 bytes) are 2-byte aligned: each run loads from the 4-byte
 //   aligned address below it and is shifted into place (v_alignbyte).
+//   Q8_0: the block pair 2g, 2g+1 (68 bytes); step t = 4blk + s takes
+//   elements 8s .. +7 of block 2g + blk (the same k as Q4_0's steps).
 //   Q4_0 / Q4_1: the block pair 2g, 2g+1 of the group (36 or 40 contiguous
 //   bytes, 4-byte aligned).  Step t = 4blk + 2nib + hf takes, in k-slice g,
 //   elements 16nib + 8hf .. +7 of block 2g + blk (low nibbles of qs bytes
@@ -75,16 +79,18 @@
 #include "vkf_device.h"
 
 #define GM_WAVES 16
-enum { GF_Q4_K = 0, GF_Q4_0 = 1, GF_Q4_1 = 2, GF_Q6_K = 3, GF_Q5_K = 4 };
+enum { GF_Q4_K = 0, GF_Q4_0 = 1, GF_Q4_1 = 2, GF_Q6_K = 3, GF_Q5_K = 4, GF_Q8_0 = 5 };
 
 // formats with a per-sub-block min term (dmin * mn), fed by the sub-block sums of x
 template <int F> constexpr bool gm_kmin() { return F == GF_Q4_K || F == GF_Q5_K; }
 
 // 256-k groups per wave held in registers at once (the most without spills)
-template <int F> constexpr int gm_maxsb() { return F == GF_Q4_K ? 5 : F == GF_Q6_K ? 1 : F == GF_Q5_K ? 3 : 4; }
+template <int F> constexpr int gm_maxsb() {
+    return F == GF_Q4_K ? 5 : F == GF_Q6_K ? 1 : (F == GF_Q5_K || F == GF_Q8_0) ? 3 : 4;
+}
 
 template <int F> constexpr uint32_t gm_group_bytes() {
-    return F == GF_Q4_1 ? 160 : F == GF_Q6_K ? 210 : F == GF_Q5_K ? 176 : 144;
+    return F == GF_Q4_1 ? 160 : F == GF_Q6_K ? 210 : F == GF_Q5_K ? 176 : F == GF_Q8_0 ? 272 : 144;
 }
 
 // k offset, within its 256-k group, of the 8 elements of MFMA step t, k-slice g
@@ -183,6 +189,11 @@ struct GmSb {
     vkf_u4 v[3];
 };
 template <>
+struct GmSb<GF_Q8_0> {
+    vkf_u4 v[4];  // bytes 0 .. 63 of the block pair
+    uint32_t e;   // bytes 64 .. 67
+};
+template <>
 struct GmSb<GF_Q5_K> {
     vkf_u4 v[4];  // header, qh run, qs runs
 };
@@ -213,6 +224,11 @@ __device__ __forceinline__ void gm_load(const uint8_t *row, uint32_t sb, int g, 
             t.e[k] = *(const uint32_t *)(a + off[k] + (k < 4 || t.sh ? 16 : 12));
         }
         t.d = *(const uint16_t *)(b + 208);
+    } else if constexpr (F == GF_Q8_0) {
+        const uint8_t *p = b + 68 * g;
+#pragma unroll
+        for (int k = 0; k < 4; k++) t.v[k] = *(const u4a4 *)(p + 16 * k);
+        t.e = *(const uint32_t *)(p + 64);
     } else if constexpr (F == GF_Q5_K) {
         t.v[0] = *(const vkf_u4 *)b;
         t.v[1] = *(const vkf_u4 *)(b + 16 + 16 * (g & 1));
@@ -247,7 +263,9 @@ __device__ __forceinline__ void gm_load_batch(const uint8_t *row, uint32_t s0, u
 }
 
 // load instructions gm_load issues
-template <int F> constexpr int gm_loads_per_group() { return F == GF_Q6_K ? 11 : F == GF_Q5_K ? 4 : 3; }
+template <int F> constexpr int gm_loads_per_group() {
+    return F == GF_Q6_K ? 11 : F == GF_Q8_0 ? 5 : F == GF_Q5_K ? 4 : 3;
+}
 
 __device__ __forceinline__ vkf_h2 gm_h2(uint32_t u) { return __builtin_bit_cast(vkf_h2, u); }
 __device__ __forceinline__ uint32_t gm_u(vkf_h2 h) { return __builtin_bit_cast(uint32_t, h); }
@@ -300,6 +318,18 @@ __device__ __forceinline__ vkf_h8 gm_decode5(uint32_t d0, uint32_t t0, uint32_t 
 #pragma unroll
     for (int p = 0; p < 4; p++)
         r[p] = gm_u(__builtin_elementwise_fma(gm_h2(gm_and_or(f[p], m5, gm_u(h[p]))), s2, n2));
+    return __builtin_bit_cast(vkf_h8, r);
+}
+
+// Q8_0: d*b of the 8 int8 codes in dwords d0, d1; d2 = {d, d}
+__device__ __forceinline__ vkf_h8 gm_decode_q8(uint32_t d0, uint32_t d1, vkf_h2 d2, uint32_t c64) {
+    const vkf_h2 m1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t u0 = d0 ^ 0x80808080u, u1 = d1 ^ 0x80808080u;
+    const uint32_t p[4] = {gm_and_or(u0, 0x00ff00ffu, c64), gm_and_or(u0 >> 8, 0x00ff00ffu, c64),
+                           gm_and_or(u1, 0x00ff00ffu, c64), gm_and_or(u1 >> 8, 0x00ff00ffu, c64)};
+    vkf_u4 r;
+#pragma unroll
+    for (int k = 0; k < 4; k++) r[k] = gm_u((gm_h2(p[k]) + m1152) * d2);
     return __builtin_bit_cast(vkf_h8, r);
 }
 
@@ -431,6 +461,31 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
                     const float d = vkf_h2f(T.d);
 #pragma unroll
                     for (int e = 0; e < 4; e++) y4[e] = fmaf(d, acc[e], y4[e]);
+                } else if constexpr (F == GF_Q8_0) {
+                    // block 0: d at bytes 0-1, codes 2 .. 33; block 1: d at 34-35, codes 36 .. 67
+                    const GmSb<F> &T = t[u];
+                    const uint32_t w[17] = {T.v[0][0], T.v[0][1], T.v[0][2], T.v[0][3], T.v[1][0], T.v[1][1],
+                                            T.v[1][2], T.v[1][3], T.v[2][0], T.v[2][1], T.v[2][2], T.v[2][3],
+                                            T.v[3][0], T.v[3][1], T.v[3][2], T.v[3][3], T.e};
+#pragma unroll
+                    for (int blk = 0; blk < 2; blk++) {
+                        const _Float16 d = gm_f16(blk ? w[8] >> 16 : w[0] & 0xffffu);
+                        const vkf_h2 d2 = {d, d};
+#pragma unroll
+                        for (int st = 0; st < 4; st++) {
+                            uint32_t c0, c1;
+                            if (blk == 0) {
+                                c0 = __builtin_amdgcn_alignbyte(w[2 * st + 1], w[2 * st], 2);
+                                c1 = __builtin_amdgcn_alignbyte(w[2 * st + 2], w[2 * st + 1], 2);
+                            } else {
+                                c0 = w[9 + 2 * st];
+                                c1 = w[10 + 2 * st];
+                            }
+                            const vkf_h8 xv = *(const vkf_h8 *)(xg + (4 * blk + st) * (4 * MR * 16));
+                            y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, gm_decode_q8(c0, c1, d2, c64), y4, 0, 0,
+                                                                        0);
+                        }
+                    }
                 } else if constexpr (gm_kmin<F>()) {
                     const vkf_u4 hdr = t[u].v[0];
                     const float dall = vkf_h2f(hdr[0] & 0xffffu), dmin = vkf_h2f(hdr[0] >> 16);
@@ -560,3 +615,4 @@ VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_0_f16(VkfGemvA
 VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_1_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_1>(a); }
 VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q6_k_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q6_K>(a); }
 VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q5_k_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q5_K>(a); }
+VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q8_0_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q8_0>(a); }
