@@ -237,6 +237,53 @@ def test_gemv_mfma_q6_k(dev, M, N, K):
     assert _per_row_err(y, x64, w, O.Q6_K, N, K) <= TOL_F32
 
 
+MFMA_ALL = [O.Q4_K, O.Q5_K, O.Q4_0, O.Q4_1, O.Q8_0, O.Q6_K]
+
+
+@pytest.mark.parametrize("qt", MFMA_ALL, ids=[O.QNAMES[q] for q in MFMA_ALL])
+@pytest.mark.parametrize("kind", ["f32", "q8_1"])
+@pytest.mark.parametrize("M", [2, 9])
+@pytest.mark.parametrize("K", [2560, 13824])
+def test_gemv_mfma_activation_kinds(dev, qt, kind, M, K):
+    """fp32 and Q8_1 activations on the matrix-core GEMV: each 16-byte piece
+    of the fp16 LDS image converted from its source (Q8_1 as fp16(d*q)),
+    K = 13824 as K-slice launches whose activation pointers advance by the
+    slice's bytes in the source format."""
+    from vkflame_amd import ops
+    N = 3001
+    w = O.gen_weight(qt, N, K, seed_for(2, 100 + qt))
+    xa, x64 = _x(kind, M, K, seed_for(2, 110 + M))
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
+    assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32
+
+
+@pytest.mark.parametrize("kind", ["f32", "q8_1"])
+def test_gemv_mfma_activation_range(dev, kind):
+    """Rows far outside fp16's range (up to ~4e6, Q8_1 d*q past 65504), a row
+    of tiny values (~1e-30), an all-zero row: the per-row power-of-two
+    scaling of the fp16 LDS image keeps every row within the tolerance."""
+    from vkflame_amd import ops
+    N, K, M = 300, 4096, 6
+    rng = np.random.default_rng(seed_for(2, 120))
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    x[0] *= 1e6
+    x[1] *= 1e-30
+    x[2] = 0.0
+    x[3, ::7] *= 3e4
+    if kind == "q8_1":
+        xa = O.np_quantize_q8_1(x).reshape(M, -1)
+        x64 = O.np_dequant(O.Q8_1, xa).reshape(M, K).astype(np.float64)
+    else:
+        xa, x64 = x, x.astype(np.float64)
+    for qt in (O.Q4_K, O.Q6_K):
+        w = O.gen_weight(qt, N, K, seed_for(2, 121 + qt))
+        y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
+        ref = O.ref_gemv(x64, O.np_dequant(qt, w).reshape(N, K))
+        assert np.all(y[2] == 0.0)
+        for m in (0, 1, 3, 4, 5):
+            assert rel_err(y[m], ref[m]) <= TOL_F32, (O.QNAMES[qt], m)
+
+
 def test_gemv_mfma_q6_k_extreme_scales(dev):
     """Every scale at -128 or 127 and codes at 0 / 63: operands of magnitude
     up to 4096, the fp16 rounding at its largest."""

@@ -34,7 +34,7 @@ constexpr int kNotSup = hipErrorNotSupported;
 // the waves per 16-row tile, from a sweep on MI355X: 4 from 1.5 tiles per CU
 // up (688 and 864 tiles: 4 beats 8 by 10-20%), 8 below (320 tiles: 8 beats
 // 4 by 20%), 16 for very few rows.
-constexpr size_t kMfmaRed = 16384;
+constexpr size_t kMfmaRed = 16384 + 64;  // K-split partials, then 16 row maxima
 
 static uint32_t mfma_split(uint32_t tiles, uint32_t cus) {
     if ((uint64_t)tiles * 2 >= (uint64_t)cus * 3) return 4;
@@ -214,7 +214,8 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
         if (xk == 1 && (!aligned(x, 16) || (ldx % 4) != 0)) return kInval;
         VkfGemvArgs a{(const uint8_t *)w, x, y, row_bytes, (uint64_t)ldx, (uint64_t)ldy,
                       (uint32_t)M, (uint32_t)N, (uint32_t)K, 0u};
-        // Q4_K, Q4_0, Q4_1, Q6_K, Q5_K, Q8_0 x fp16 at 2 <= M <= 16 on the matrix cores
+        // Q4_K, Q4_0, Q4_1, Q6_K, Q5_K, Q8_0 at 2 <= M <= 16 on the matrix cores
+        // (fp32 and Q8_1 activations converted to the fp16 LDS image)
         // (kernels/gemv_mfma.hip; faster than the dot GEMV from M = 2 up,
         // e.g. Q4_0 11008x4096 M=4 13.2 vs 16.9 us on MI355X): the
         // activations of a K slice staged for 8 or 16 rows (512 bytes per
@@ -231,11 +232,13 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
         const bool kmin = mf == 0 || mf == 4;  // Q4_K / Q5_K: sub-block sums of x staged too
         // Q8_0 at M <= 4 stays on the dot GEMV unless N gives two tiles per CU
         // (4096x4096 M=4: 11.6 us there against 13.2 here; 13824x5120 M=4:
-        // 25.5 against 21.9)
-        const bool mf_ok = mf != 5 || M > 4 || cdiv(N, 16) >= 2u * (uint32_t)vkf::cu_count();
+        // 25.5 against 21.9); so do fp32 activations at M <= 4 where the dot
+        // GEMV takes the format (Q4_K 13824x5120 M=2: 17.2 against 20.6 us)
+        const bool mf_ok = (mf != 5 || M > 4 || cdiv(N, 16) >= 2u * (uint32_t)vkf::cu_count()) &&
+                           !(xk == 1 && M <= 4 && dot_format(qt) >= 0);
         const uint32_t mr = M <= 8 ? 8 : 16, ga = kmin ? 16 : 4;
         const size_t per_group = (size_t)mr * (kmin ? 544 : 512);
-        if (mf >= 0 && mf_ok && M >= 2 && xk == 0 && (K % 256) == 0 && aligned(w, ga) && (row_bytes % ga) == 0 &&
+        if (mf >= 0 && mf_ok && M >= 2 && (K % 256) == 0 && aligned(w, ga) && (row_bytes % ga) == 0 &&
             vkf::max_lds() >= kMfmaRed + per_group) {
             const uint32_t nsb = (uint32_t)(K / 256), cap = (uint32_t)((vkf::max_lds() - kMfmaRed) / per_group);
             const uint32_t slices = cdiv(nsb, cap), per = cdiv(nsb, slices);
@@ -243,12 +246,15 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
             const uint32_t P = mfma_split(tiles, cus);
             const uint32_t G = 16 / P, grid = cdiv(tiles, G) < cus ? cdiv(tiles, G) : cus;
             const uint64_t group_bytes = mf == 2 ? 160 : mf == 3 ? 210 : mf == 4 ? 176 : mf == 5 ? 272 : 144;
-            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_MFMA_Q4_K_F16 + mf);
+            // kernel table: the six formats with fp16, then fp32, then Q8_1 activations
+            static_assert(VKF_K_GEMV_MFMA_Q8_0_Q81 == VKF_K_GEMV_MFMA_Q4_K_F16 + 17, "matrix-core GEMV table order");
+            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_MFMA_Q4_K_F16 + mf + 6 * xk);
+            const uint64_t x_group_bytes = xk == 0 ? 512 : xk == 1 ? 1024 : 288;  // 256 k of one row
             for (uint32_t s0 = 0; s0 < nsb; s0 += per) {
                 const uint32_t n_sb = nsb - s0 < per ? nsb - s0 : per;
                 VkfGemvArgs b = a;
                 b.w = a.w + group_bytes * s0;
-                b.x = (const uint16_t *)x + (uint64_t)s0 * 256;
+                b.x = (const uint8_t *)x + x_group_bytes * s0;
                 b.K = n_sb * 256;
                 b.flags = (P << 8) | (a.flags & 1u) | (s0 > 0 ? 1u : 0u);
                 const int rc = vkf::launch(k, dim3(grid), dim3(1024), b, S(stream), kMfmaRed + per_group * n_sb);

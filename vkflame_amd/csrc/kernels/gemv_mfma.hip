@@ -1,6 +1,8 @@
 // gemv_mfma.hip — small-batch GEMV (2 <= M <= 16) of Q4_K, Q5_K, Q4_0, Q4_1,
-// Q8_0 and Q6_K weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T, fp16
-// activations.
+// Q8_0 and Q6_K weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T,
+// with fp16, fp32 or Q8_1 activations (the latter two staged in LDS as
+// fp16: fp32 rounded once, Q8_1 as fp16(d*q), the value the prefill GEMM's
+// activation decode produces).
 //
 // With 2..16 activation rows the VALU dot product costs M multiply-adds per
 // weight; a 16x16x32 fp16 MFMA takes 16 weight rows x 32 k against up to 16
@@ -119,6 +121,79 @@ __device__ __forceinline__ uint32_t gm_k0(uint32_t t, uint32_t g) {
 // = lane of a 1 KiB load), then a pass reorders the halves of every piece
 // (and, for Q4_K, writes the sub-block sums).
 template <int F> constexpr uint32_t gm_xs_bytes_per_group(uint32_t MR) { return gm_kmin<F>() ? 32 * MR : 0; }
+
+// fp32 or Q8_1 activations (XK = 1, 2) are staged per row scaled by a power
+// of two that puts the row's largest magnitude in [2^14, 2^15): fp16 holds
+// any fp32 row without overflow (nor, relative to the row's maximum, loss
+// below 2^-24), and Q8_1 rows with d*127 past 65504 likewise.  The scaling
+// is exact; y is unscaled per row in the epilogue.  Row maxima (fp32 bits,
+// 16 words) sit after the K-split partials.
+template <int F, uint32_t MR>
+__device__ __forceinline__ uint32_t *gm_row_max(const VkfGemvArgs &a, unsigned char *lds) {
+    return (uint32_t *)(lds + (uint64_t)a.K * MR * 2 + (uint64_t)(a.K / 256) * gm_xs_bytes_per_group<F>(MR) + 16384);
+}
+
+__device__ __forceinline__ float gm_row_scale(uint32_t mx_bits) {
+    const float mx = __builtin_bit_cast(float, mx_bits);
+    int e;
+    (void)frexpf(mx, &e);
+    return mx > 0.0f ? ldexpf(1.0f, 15 - e < 126 ? 15 - e : 126) : 1.0f;
+}
+
+// each 16-byte piece of the fp16 LDS image (8 consecutive k of one row, at
+// the position the direct loads give it) converted by one thread
+template <int F, uint32_t MR, int XK>
+__device__ __forceinline__ void gm_convert_x(const VkfGemvArgs &a, unsigned char *lds) {
+    uint32_t *rmax = gm_row_max<F, MR>(a, lds);
+    if (threadIdx.x < MR) rmax[threadIdx.x] = 0;
+    __syncthreads();
+    {
+        // blockDim.x / MR threads per row, one LDS atomic each
+        const uint32_t row = threadIdx.x % MR, rr = row < a.M ? row : a.M - 1;
+        float mx = 0.0f;
+        if constexpr (XK == 1) {
+            const float *src = (const float *)a.x + (uint64_t)rr * a.ldx;
+            for (uint32_t c = threadIdx.x / MR; c < a.K / 4; c += blockDim.x / MR) {
+                const vkf_f4 v = *(const vkf_f4 *)(src + 4 * c);
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+            }
+        } else {
+            const uint8_t *src = (const uint8_t *)a.x + (uint64_t)rr * a.ldx;
+            for (uint32_t b = threadIdx.x / MR; b < a.K / 32; b += blockDim.x / MR)
+                mx = fmaxf(mx, fabsf(vkf_h2f(*(const uint16_t *)(src + 36ull * b))));
+            mx *= 127.0f;
+        }
+        atomicMax(&rmax[row], __builtin_bit_cast(uint32_t, mx));  // non-negative floats order as integers
+    }
+    __syncthreads();
+    const uint32_t pieces = MR * a.K / 8;
+    for (uint32_t P = threadIdx.x; P < pieces; P += blockDim.x) {
+        const uint32_t i = P % MR, g = (P / MR) & 3, s = P / (4 * MR);
+        const uint32_t row = i < a.M ? i : a.M - 1, k0 = (s >> 3) * 256 + gm_k0<F>(s & 7, g);
+        const float sc = gm_row_scale(rmax[i]);
+        vkf_h8 h;
+        if constexpr (XK == 1) {
+            const float *src = (const float *)a.x + (uint64_t)row * a.ldx + k0;
+            const vkf_f4 v0 = *(const vkf_f4 *)src, v1 = *(const vkf_f4 *)(src + 4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                h[e] = (_Float16)(v0[e] * sc);
+                h[4 + e] = (_Float16)(v1[e] * sc);
+            }
+        } else {
+            // Q8_1 block k0/32: d (fp16) at byte 0, codes at 4 .. 35
+            const uint8_t *blk = (const uint8_t *)a.x + (uint64_t)row * a.ldx + (uint64_t)(k0 / 32) * 36;
+            const float d = vkf_h2f(*(const uint16_t *)blk) * sc;
+            const uint32_t q0 = *(const uint32_t *)(blk + 4 + k0 % 32), q1 = *(const uint32_t *)(blk + 8 + k0 % 32);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                h[e] = (_Float16)(d * (float)(int8_t)(q0 >> (8 * e)));
+                h[4 + e] = (_Float16)(d * (float)(int8_t)(q1 >> (8 * e)));
+            }
+        }
+        *(vkf_h8 *)(lds + (uint64_t)P * 16) = h;
+    }
+}
 
 // the x pieces of the workgroup's 1 KiB direct load c
 template <int F, uint32_t MR>
@@ -373,7 +448,7 @@ __device__ __forceinline__ vkf_h8 gm_decode_q6(uint32_t d0, uint32_t d1, uint32_
     return __builtin_bit_cast(vkf_h8, r);
 }
 
-template <int F, uint32_t MR>
+template <int F, uint32_t MR, int XK>
 __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *smem) {
     const uint32_t nsb = a.K / 256;
     const uint32_t P = (a.flags >> 8) & 0xffu;  // waves per tile: 4, 8 or 16
@@ -393,7 +468,12 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
     constexpr int MAXSB = gm_maxsb<F>();
     GmSb<F> t[MAXSB];
     const uint32_t nc = MR * a.K * 2 / 1024;  // 1 KiB loads of x (MR * K * 2 is a multiple of 4096)
-    for (uint32_t c = wave; c < nc; c += GM_WAVES) gm_dma_x<F, MR>(a, smem, c, lane);
+    if constexpr (XK == 0) {
+        for (uint32_t c = wave; c < nc; c += GM_WAVES) gm_dma_x<F, MR>(a, smem, c, lane);
+    } else {
+        (void)nc;
+        gm_convert_x<F, MR, XK>(a, smem);
+    }
     asm volatile("" ::: "memory");
     {
         const uint32_t n = (blockIdx.x * G + grp) * 16 + li;
@@ -594,8 +674,10 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
             for (int e = 0; e < 4; e++) {
                 const uint32_t m = 4 * lg + e;
                 if (m < a.M && n < a.N) {
+                    float v = s[e];
+                    if constexpr (XK != 0) v *= 1.0f / gm_row_scale(gm_row_max<F, MR>(a, smem)[m]);  // exact
                     float *yp = a.y + (uint64_t)m * a.ldy + n;
-                    *yp = (a.flags & 1u) ? *yp + s[e] : s[e];
+                    *yp = (a.flags & 1u) ? *yp + v : v;
                 }
             }
         }
@@ -603,16 +685,26 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
     }
 }
 
-template <int F>
+template <int F, int XK>
 __device__ __forceinline__ void gemv_mfma_entry(const VkfGemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    if (a.M <= 8) gemv_mfma<F, 8>(a, smem);
-    else gemv_mfma<F, 16>(a, smem);
+    if (a.M <= 8) gemv_mfma<F, 8, XK>(a, smem);
+    else gemv_mfma<F, 16, XK>(a, smem);
 }
 
-VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_k_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_K>(a); }
-VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_0_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_0>(a); }
-VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q4_1_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q4_1>(a); }
-VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q6_k_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q6_K>(a); }
-VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q5_k_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q5_K>(a); }
-VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_q8_0_f16(VkfGemvArgs a) { gemv_mfma_entry<GF_Q8_0>(a); }
+#define VKF_GEMV_MFMA(name, F)                                                                            \
+    VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_##name##_f16(VkfGemvArgs a) {           \
+        gemv_mfma_entry<F, 0>(a);                                                                         \
+    }                                                                                                     \
+    VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_##name##_f32(VkfGemvArgs a) {           \
+        gemv_mfma_entry<F, 1>(a);                                                                         \
+    }                                                                                                     \
+    VKF_KERNEL void __launch_bounds__(64 * GM_WAVES) vkf_gemv_mfma_##name##_q8_1(VkfGemvArgs a) {          \
+        gemv_mfma_entry<F, 2>(a);                                                                         \
+    }
+VKF_GEMV_MFMA(q4_k, GF_Q4_K)
+VKF_GEMV_MFMA(q4_0, GF_Q4_0)
+VKF_GEMV_MFMA(q4_1, GF_Q4_1)
+VKF_GEMV_MFMA(q6_k, GF_Q6_K)
+VKF_GEMV_MFMA(q5_k, GF_Q5_K)
+VKF_GEMV_MFMA(q8_0, GF_Q8_0)
