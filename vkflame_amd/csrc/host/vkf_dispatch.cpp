@@ -90,12 +90,17 @@ const uint32_t kDotAlign[5] = {4, 8, 4, 16, 16};
 
 // Lanes per row segment.  A wave tile is (64/S)*rpl rows; a lane walks
 // ceil(C/S) chunks per tile and a wave ceil(tiles/slots) tiles, so the
-// critical path is their product; ties go to the larger S (more tiles).
+// critical path is their product plus each tile's fixed work; ties go to
+// the larger S (more tiles).
 uint32_t dot_segment(uint32_t N, uint32_t C, uint32_t rpl, uint32_t slots) {
     uint32_t best = 64, best_cost = 0xffffffffu;
     for (uint32_t s = 64; s >= 8; s >>= 1) {
         const uint32_t tiles = cdiv(N, (64 / s) * rpl);
-        const uint32_t cost = cdiv(tiles, slots) * cdiv(C, s);
+        // rounds of tiles over the wave slots x (chunks per lane + 1.5 for a
+        // tile's fixed work: the lane reduction and the y store), in halves.
+        // Measured on MI355X, Q4_1 11008x4096 M=1: S = 16 7.5 us against
+        // S = 64 8.3 us, which the chunk count alone prefers.
+        const uint32_t cost = cdiv(tiles, slots) * (2 * cdiv(C, s) + 3);
         if (cost < best_cost) {
             best_cost = cost;
             best = s;
