@@ -213,12 +213,15 @@ def test_config5_q6_k_q8_1_prefill(dev):
 @pytest.mark.parametrize("qt", WTYPES, ids=[O.QNAMES[q] for q in WTYPES])
 def test_gemm_q_fp16_wide_tiles(dev, qt):
     """M >= 256 takes 256-row tiles (512 threads, weight tile decoded once per
-    256 rows); M < 256 the 128-row tiles.  Both multiply the same fp16 operand
-    values in the same MFMA order, so the first 255 rows of an M = 300 product
-    equal the M = 255 product bit for bit; both match the oracle."""
+    256 rows) when they fill at least half the CUs; M < 256 the 128-row
+    tiles.  Both multiply the same fp16 operand values in the same MFMA
+    order, so the first 255 rows of an M = 300 product equal the M = 255
+    product bit for bit; both match the oracle.  N = 8200: 2 x 65 wide
+    tiles, enough for the wide kernel on a 256-CU MI355X."""
     import torch
     from vkflame_amd import ops
-    N, K = 333, 1024
+    N, K = 8200, 1024
+    assert 2 * 2 * -(-N // 128) >= torch.cuda.get_device_properties(0).multi_processor_count
     w = O.gen_weight(qt, N, K, seed_for(3, 90 + qt))
     x = _f16(np.random.default_rng(seed_for(3, 100 + qt)), 300, K)
     wd, xd = to_dev(w, dev), to_dev(x, dev)
