@@ -307,7 +307,6 @@ template <int ES, class ACC>
 __device__ __forceinline__ void gemm_mainloop_dma(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, ACC acc[4][4],
                                                   uint8_t *smem) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wr = wave >> 1, wc = wave & 1;
-    const int li = lane & 15, lg = lane >> 4;
     const uint32_t nk = (uint32_t)(((uint64_t)a.K * ES) / 128);
     const uint8_t *gx[4], *gy[4];
 #pragma unroll
@@ -331,7 +330,6 @@ __device__ __forceinline__ void gemm_mainloop_dma(const VkfGemmArgs &a, uint32_t
 #pragma unroll
     for (uint32_t s = 0; s + 1 < GNST; s++)
         if (s < nk) issue(s, s);
-    const int sw = li & 7;
     for (uint32_t kt = 0; kt < nk; kt++) {
         // this thread's loads of step kt are done when at most the loads of
         // the (up to GNST-2) later steps are outstanding
@@ -836,7 +834,6 @@ template <int QT>
 __device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, vkf_f4 acc[4][4],
                                                    uint8_t *smem) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wr = wave >> 1, wc = wave & 1;
-    const int li = lane & 15, lg = lane >> 4;
     const uint32_t nk = a.K / 64;
     const uint8_t *gx[4];
 #pragma unroll
@@ -866,7 +863,6 @@ __device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_
     store_y(0, ty);
     wait_vm<0>();
     __syncthreads();
-    const int sw = li & 7;
     for (uint32_t kt = 0; kt < nk; kt++) {
         const uint32_t cur = kt & 1;
         if (kt + 1 < nk) {
