@@ -216,12 +216,15 @@ def test_gemm_q_fp16_wide_tiles(dev, qt):
     256 rows) when they fill at least half the CUs; M < 256 the 128-row
     tiles.  Both multiply the same fp16 operand values in the same MFMA
     order, so the first 255 rows of an M = 300 product equal the M = 255
-    product bit for bit; both match the oracle.  N = 8200: 2 x 65 wide
-    tiles, enough for the wide kernel on a 256-CU MI355X."""
+    product bit for bit; both match the oracle.  N = 16600: 2 x 130 wide
+    tiles, enough for the wide kernel on a 256-CU MI355X, and 2 x 130
+    128-row tiles at M = 255, more than one per CU (fewer would take the
+    split-K kernel, whose two partial sums round differently)."""
     import torch
     from vkflame_amd import ops
-    N, K = 8200, 1024
-    assert 2 * 2 * -(-N // 128) >= torch.cuda.get_device_properties(0).multi_processor_count
+    N, K = 16600, 1024
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert 2 * 2 * -(-N // 128) >= cus and 2 * -(-N // 128) > cus
     w = O.gen_weight(qt, N, K, seed_for(3, 90 + qt))
     x = _f16(np.random.default_rng(seed_for(3, 100 + qt)), 300, K)
     wd, xd = to_dev(w, dev), to_dev(x, dev)
@@ -242,9 +245,11 @@ def test_gemm_q_q8_1_workspace_paths(dev, qt, M, K):
     GEMM), into a stream-ordered allocation of the library's
     (vkflame_dispatch_gemm_q), or per tile inside the Q8_1 GEMM (no
     workspace).  Every route multiplies the same fp16 operand values in the
-    same MFMA order: the two workspace routes agree bit for bit, the per-tile
-    route too where all take the direct-to-LDS main loops (K % 64 == 0), and
-    all match the oracle."""
+    same MFMA order: the two workspace routes agree bit for bit, and all
+    match the oracle.  The per-tile route adds K in one sequence; on these
+    small grids (at most one 128 x 128 tile per CU) the fp16-activation
+    route splits K between two wave groups, so those two agree to rounding
+    (bit for bit on larger grids)."""
     import torch
     from vkflame_amd import ops
     from vkflame_amd import _lib as L
@@ -264,8 +269,7 @@ def test_gemm_q_q8_1_workspace_paths(dev, qt, M, K):
     torch.cuda.synchronize()
     a, b, c = y_ws.cpu().numpy(), y_tile.cpu().numpy(), y_lib.cpu().numpy()
     assert bits_equal(a, c), first_mismatch(a, c)
-    if K % 64 == 0:
-        assert bits_equal(a, b), first_mismatch(a, b)
+    assert rel_err(a, b) <= 1e-5
     x64 = O.np_dequant(O.Q8_1, xq).reshape(M, K).astype(np.float64)
     ref = O.ref_gemv(x64, O.np_dequant(qt, w).reshape(N, K))
     for y in (a, b, c):

@@ -353,6 +353,14 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
                            S(stream));
     }
     dim3 grid(cdiv(N, 128), cdiv(M, 128));
+    // 128-row grids of at most one tile per CU: the 512-thread kernel that
+    // splits K between two wave groups (kernels/gemm.hip
+    // gemm_mainloop_qdma_k2), same direct-to-LDS conditions as above
+    if (xk == 0 && aligned(x, 16) && (ldx % 8) == 0 && (K % 64) == 0 &&
+        (uint64_t)grid.x * grid.y <= (uint64_t)vkf::cu_count()) {
+        const int fi = (gemm_kernel(qt, 0) - VKF_K_GEMM_Q4_0_F16) / 2;
+        return vkf::launch((VkfKernelId)(VKF_K_GEMM_K2_Q4_0_F16 + fi), grid, dim3(512), g, S(stream));
+    }
     return vkf::launch(gemm_kernel(qt, xk), grid, dim3(256), g, S(stream));
 }
 

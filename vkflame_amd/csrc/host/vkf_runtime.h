@@ -131,7 +131,14 @@
     X(GEMM_W_Q5_0_F16, "vkf_gemm_q5_0_f16_w")               \
     X(GEMM_W_Q4_K_F16, "vkf_gemm_q4_k_f16_w")               \
     X(GEMM_W_Q5_K_F16, "vkf_gemm_q5_k_f16_w")               \
-    X(GEMM_W_Q6_K_F16, "vkf_gemm_q6_k_f16_w")
+    X(GEMM_W_Q6_K_F16, "vkf_gemm_q6_k_f16_w")             \
+    X(GEMM_K2_Q4_0_F16, "vkf_gemm_q4_0_f16_k2")             \
+    X(GEMM_K2_Q4_1_F16, "vkf_gemm_q4_1_f16_k2")             \
+    X(GEMM_K2_Q8_0_F16, "vkf_gemm_q8_0_f16_k2")             \
+    X(GEMM_K2_Q5_0_F16, "vkf_gemm_q5_0_f16_k2")             \
+    X(GEMM_K2_Q4_K_F16, "vkf_gemm_q4_k_f16_k2")             \
+    X(GEMM_K2_Q5_K_F16, "vkf_gemm_q5_k_f16_k2")             \
+    X(GEMM_K2_Q6_K_F16, "vkf_gemm_q6_k_f16_k2")
 
 enum VkfKernelId {
 #define VKF_X(id, sym) VKF_K_##id,

@@ -1256,6 +1256,28 @@ GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a) {
 #define GEMM_K2_LDS (2 * 65536)
 #define GEMM_KERNEL_K2 VKF_KERNEL void __launch_bounds__(512)
 
+// Split-K workgroups: group 1's (waves 4-7) accumulators -> LDS (lane-major,
+// 64 KiB), group 0 adds them; ends with LDS free.  smem must be free.
+template <class ACC>
+__device__ __forceinline__ void k2_group_sum(ACC acc[4][4], uint8_t *smem) {
+    const int wave = threadIdx.x >> 6, g = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
+    vkf_i4 *red = (vkf_i4 *)smem;
+    if (g == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) red[(wq * 16 + 4 * i + j) * 64 + lane] = __builtin_bit_cast(vkf_i4, acc[i][j]);
+    }
+    __syncthreads();
+    if (g == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] += __builtin_bit_cast(ACC, red[(wq * 16 + 4 * i + j) * 64 + lane]);
+    }
+    __syncthreads();  // LDS free for the epilogue
+}
+
 template <int ES, class ACC>
 __device__ __forceinline__ void gemm_mainloop_dma_k2(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, ACC acc[4][4],
                                                      uint8_t *smem) {
@@ -1295,22 +1317,7 @@ __device__ __forceinline__ void gemm_mainloop_dma_k2(const VkfGemmArgs &a, uint3
         }
     }
     __syncthreads();  // LDS free for the reduction
-    // group 1's accumulators -> LDS (lane-major, 64 KiB), group 0 adds them
-    vkf_i4 *red = (vkf_i4 *)smem;
-    if (g == 1) {
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) red[(wq * 16 + 4 * i + j) * 64 + lane] = __builtin_bit_cast(vkf_i4, acc[i][j]);
-    }
-    __syncthreads();
-    if (g == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) acc[i][j] += __builtin_bit_cast(ACC, red[(wq * 16 + 4 * i + j) * 64 + lane]);
-    }
-    __syncthreads();  // LDS free for the epilogue
+    k2_group_sum(acc, smem);
 }
 
 // epilogue of the split-K kernels: group 0 stages the tile, all 512 threads store it
@@ -1370,3 +1377,95 @@ GEMM_KERNEL_K2 vkf_gemm_i8_k2(VkfGemmArgs a) {
                 }
             }
 }
+
+// ---------------------------------------------------------------------------
+// Quantised-weight GEMM with fp16 activations, K split inside the workgroup
+// as in vkf_gemm_f16_k2: for grids of at most one 128 x 128 tile per CU
+// (the down projections of a prefill, N = 4096..5120 at M = 512).  Group g
+// (waves 4g..4g+3) loads the activation tile and decodes the weight tile of
+// the K steps kt = g (mod 2) into its own half of each stage (QStage, the
+// same values as the 256-thread kernel; group 1's threads see rows from
+// threadIdx.x / 2 - 128 through row0 - 128); the two partial tiles meet in
+// LDS at the end.  Needs the direct-to-LDS activation loads (16-byte aligned
+// rows, K % 64 == 0; the host checks).
+// ---------------------------------------------------------------------------
+template <int QT>
+__device__ __forceinline__ void gemm_mainloop_qdma_k2(const VkfGemmArgs &a, uint32_t r0, uint32_t c0,
+                                                      vkf_f4 acc[4][4], uint8_t *smem) {
+    const int wave = threadIdx.x >> 6, g = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
+    const int wr = wq >> 1, wc = wq & 1;
+    const uint32_t nk = a.K / 64, npair = (nk + 1) / 2;
+    const uint8_t *gx[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t rr = (4 * wq + j) * 8 + (lane >> 3);
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t rx = r0 + rr < a.R ? r0 + rr : a.R - 1;
+        gx[j] = (const uint8_t *)a.X + (uint64_t)rx * a.ldx * 2 + ch * 16;
+    }
+    auto issue_x = [&](uint32_t kt, uint32_t st) {
+        uint8_t *sx = smem + st * 65536 + g * 32768;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            vkf_load_lds16(gx[j] + (uint64_t)kt * 128, sx + (4 * wq + j) * 1024);
+    };
+    const uint32_t yr = (threadIdx.x & 255) >> 1, yh = threadIdx.x & 1;
+    auto store_y = [&](uint32_t st, const TileRegs &t) {
+        uint8_t *sy = smem + st * 65536 + g * 32768 + 16384 + yr * 128;
+#pragma unroll
+        for (int k = 0; k < 4; k++) *(vkf_i4 *)(sy + (((4 * yh + k) ^ (yr & 7)) << 4)) = t.v[k];
+    };
+    const uint32_t qrow0 = c0 - 128u * (uint32_t)g;  // + threadIdx.x / 2 (mod 2^32) = c0 + row in the tile
+    QStage<QT> q;
+    TileRegs ty;
+    if ((uint32_t)g < nk) {
+        issue_x(g, 0);
+        q.load((const uint8_t *)a.Y, a.ldy, a.Cn, qrow0, a.K, 64u * g);
+        q.decode(ty);
+        store_y(0, ty);
+    }
+    wait_vm<0>();
+    __syncthreads();
+    for (uint32_t t = 0; t < npair; t++) {
+        const uint32_t cur = t & 1, kn = 2 * (t + 1) + g;
+        if (kn < nk) {
+            issue_x(kn, cur ^ 1);
+            q.load((const uint8_t *)a.Y, a.ldy, a.Cn, qrow0, a.K, kn * 64);
+        }
+        if (2 * t + g < nk) {
+            const uint8_t *lx = smem + cur * 65536 + g * 32768;
+            mfma_step_swz<2>(lx, lx + 16384, wr, wc, acc);
+        }
+        if (kn < nk) {
+            q.decode(ty);
+            store_y(cur ^ 1, ty);
+        }
+        wait_vm<0>();
+        __syncthreads();
+    }
+    k2_group_sum(acc, smem);
+}
+
+template <int QT>
+__device__ __forceinline__ void gemm_q_k2_body(const VkfGemmArgs &a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_K2_LDS];
+    uint32_t r0, c0;
+    gemm_tile_of(r0, c0);
+    vkf_f4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
+    gemm_mainloop_qdma_k2<QT>(a, r0, c0, acc, smem);
+    epilogue_tile_k2(a, r0, c0, acc, smem);
+}
+
+#define VKF_GEMM_Q_K2(name, QT) \
+    GEMM_KERNEL_K2 vkf_gemm_##name##_f16_k2(VkfGemmArgs a) { gemm_q_k2_body<QT>(a); }
+VKF_GEMM_Q_K2(q4_0, VKF_Q4_0)
+VKF_GEMM_Q_K2(q4_1, VKF_Q4_1)
+VKF_GEMM_Q_K2(q8_0, VKF_Q8_0)
+VKF_GEMM_Q_K2(q5_0, VKF_Q5_0)
+VKF_GEMM_Q_K2(q4_k, VKF_Q4_K)
+VKF_GEMM_Q_K2(q5_k, VKF_Q5_K)
+VKF_GEMM_Q_K2(q6_k, VKF_Q6_K)
