@@ -164,6 +164,26 @@ def test_gemm_q_fp16_prefill(dev, qt):
     assert rel_err(y.cpu().numpy(), ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("qt,K", [(O.Q4_0, 64), (O.Q4_0, 1088), (O.Q8_0, 192), (O.Q5_0, 1088), (O.Q4_1, 320),
+                                  (O.Q4_K, 256), (O.Q4_K, 768), (O.Q5_K, 1280), (O.Q6_K, 512)],
+                         ids=["q4_0-k64", "q4_0-k1088", "q8_0-k192", "q5_0-k1088", "q4_1-k320", "q4_k-k256",
+                              "q4_k-k768", "q5_k-k1280", "q6_k-k512"])
+def test_gemm_q_split_k_edges(dev, qt, K):
+    """Grids of at most one 128 x 128 tile per CU take the split-K kernel
+    (two wave groups on alternate 64-k steps): one step (K = 64), odd step
+    counts (group 1 idle on the last pair), ragged M and N, against the
+    oracle."""
+    import torch
+    from vkflame_amd import ops
+    M, N = 100, 203
+    w = O.gen_weight(qt, N, K, seed_for(3, 110 + qt) + K)
+    x = _f16(np.random.default_rng(seed_for(3, 120 + qt) + K), M, K)
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(x, dev), N, K)
+    torch.cuda.synchronize()
+    ref = O.ref_gemv(x.astype(np.float64), O.np_dequant(qt, w).reshape(N, K))
+    assert rel_err(y.cpu().numpy(), ref) <= TOL_F32
+
+
 @pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_K, O.Q8_0], ids=["q4_0", "q4_k", "q8_0"])
 def test_gemm_q_q8_1_activations_prefill(dev, qt):
     import torch
