@@ -344,10 +344,13 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
     // M = 256 with fp16 activations that suit its direct-to-LDS loads
     // (16-byte aligned rows, K % 64 == 0): each weight tile decoded once per
     // 256 activation rows.  Not when they would occupy fewer than half the
-    // CUs: twice as many 128-row tiles ran faster there (Q4_K 512 x 5120 x
-    // 13824 on MI355X: 227 against 250 us).
+    // CUs (twice as many 128-row tiles ran faster: Q4_K 512 x 5120 x 13824
+    // on MI355X 227 against 250 us), nor when the 128-row grid fits the CUs
+    // once, where the split-K kernel below is faster still (512 x 8192 x
+    // 5120: 77.7 against 105.8 us wide).
     if (M >= 256 && xk == 0 && aligned(x, 16) && (ldx % 8) == 0 && (K % 64) == 0 &&
-        2ull * cdiv(N, 128) * cdiv(M, 256) >= (uint64_t)vkf::cu_count()) {
+        2ull * cdiv(N, 128) * cdiv(M, 256) >= (uint64_t)vkf::cu_count() &&
+        (uint64_t)cdiv(N, 128) * cdiv(M, 128) > (uint64_t)vkf::cu_count()) {
         const int fi = (gemm_kernel(qt, 0) - VKF_K_GEMM_Q4_0_F16) / 2;
         return vkf::launch((VkfKernelId)(VKF_K_GEMM_W_Q4_0_F16 + fi), dim3(cdiv(N, 128), cdiv(M, 256)), dim3(512), g,
                            S(stream));
