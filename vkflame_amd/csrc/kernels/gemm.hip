@@ -888,27 +888,47 @@ __device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_
 // ends with a barrier).
 // epi_stage: one wave's 64x64 values (position wr, wc inside the 128x128
 // tile at r0, c0) finished and written to the fp32 staging tile.
-template <class ACC>
-__device__ __forceinline__ void epi_stage(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC acc[4][4],
-                                          float *tile, int wr, int wc) {
-    constexpr int TP = 132;
+// The epilogue's per-column scale and bias and per-row scale of one wave's
+// 64x64 values, loaded ahead (before the main loop) so that their latency
+// hides under the MFMAs instead of following them.
+struct EpiPre {
+    float cs[4], bc[4], rs[16];
+};
+__device__ __forceinline__ EpiPre epi_prefetch(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, int wr, int wc) {
     const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
-    float csv[4], bcv[4];
+    EpiPre p;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const uint32_t c = c0 + wc * 64 + 16 * j + li, cc = c < a.Cn ? c : a.Cn - 1;
-        csv[j] = a.cs ? a.cs[(a.flags & VKF_GF_CS_SCALAR) ? 0 : cc] : 1.0f;
-        bcv[j] = 0.0f;
+        p.cs[j] = a.cs ? a.cs[(a.flags & VKF_GF_CS_SCALAR) ? 0 : cc] : 1.0f;
+        p.bc[j] = 0.0f;
         if (a.bias && !(a.flags & VKF_GF_BIAS_ROW))
-            bcv[j] = (a.flags & VKF_GF_BIAS_F32) ? ((const float *)a.bias)[cc] : (float)((const _Float16 *)a.bias)[cc];
+            p.bc[j] = (a.flags & VKF_GF_BIAS_F32) ? ((const float *)a.bias)[cc] : (float)((const _Float16 *)a.bias)[cc];
     }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t r = r0 + wr * 64 + 16 * i + 4 * lg + e, rr = r < a.R ? r : a.R - 1;
+            p.rs[4 * i + e] = a.rs ? a.rs[(a.flags & VKF_GF_RS_SCALAR) ? 0 : rr] : 1.0f;
+        }
+    return p;
+}
+
+template <class ACC>
+__device__ __forceinline__ void epi_stage(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC acc[4][4],
+                                          float *tile, int wr, int wc, const EpiPre *pre = nullptr) {
+    constexpr int TP = 132;
+    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+    const EpiPre p = pre ? *pre : epi_prefetch(a, r0, c0, wr, wc);
+    const float *csv = p.cs, *bcv = p.bc;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int tr = wr * 64 + 16 * i + 4 * lg + e;
             const uint32_t r = r0 + tr, rr = r < a.R ? r : a.R - 1;
-            const float rsv = a.rs ? a.rs[(a.flags & VKF_GF_RS_SCALAR) ? 0 : rr] : 1.0f;
+            const float rsv = p.rs[4 * i + e];
             float brv = 0.0f;
             if (a.bias && (a.flags & VKF_GF_BIAS_ROW))
                 brv = (a.flags & VKF_GF_BIAS_F32) ? ((const float *)a.bias)[rr] : (float)((const _Float16 *)a.bias)[rr];
@@ -1323,9 +1343,9 @@ __device__ __forceinline__ void gemm_mainloop_dma_k2(const VkfGemmArgs &a, uint3
 // epilogue of the split-K kernels: group 0 stages the tile, all 512 threads store it
 template <class ACC>
 __device__ __forceinline__ void epilogue_tile_k2(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC acc[4][4],
-                                                 uint8_t *smem) {
+                                                 uint8_t *smem, const EpiPre *pre = nullptr) {
     const int wave = threadIdx.x >> 6;
-    if (wave < 4) epi_stage(a, r0, c0, acc, (float *)smem, (wave & 3) >> 1, wave & 1);
+    if (wave < 4) epi_stage(a, r0, c0, acc, (float *)smem, (wave & 3) >> 1, wave & 1, pre);
     __syncthreads();
     epi_store<512>(a, r0, c0, (const float *)smem);
 }
@@ -1339,8 +1359,11 @@ GEMM_KERNEL_K2 vkf_gemm_f16_k2(VkfGemmArgs a) {
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
+    const int wave = threadIdx.x >> 6;
+    EpiPre pre{};
+    if (wave < 4) pre = epi_prefetch(a, r0, c0, wave >> 1, wave & 1);  // group 0 stages the tile
     gemm_mainloop_dma_k2<2>(a, r0, c0, acc, smem);
-    epilogue_tile_k2(a, r0, c0, acc, smem);
+    epilogue_tile_k2(a, r0, c0, acc, smem, &pre);
 }
 
 GEMM_KERNEL_K2 vkf_gemm_i8_k2(VkfGemmArgs a) {
@@ -1352,9 +1375,12 @@ GEMM_KERNEL_K2 vkf_gemm_i8_k2(VkfGemmArgs a) {
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = vkf_i4{0, 0, 0, 0};
+    const int wv = threadIdx.x >> 6;
+    EpiPre pre{};
+    if (wv < 4 && !(a.flags & VKF_GF_D_I32)) pre = epi_prefetch(a, r0, c0, wv >> 1, wv & 1);
     gemm_mainloop_dma_k2<1>(a, r0, c0, acc, smem);
     if (!(a.flags & VKF_GF_D_I32)) {
-        epilogue_tile_k2(a, r0, c0, acc, smem);
+        epilogue_tile_k2(a, r0, c0, acc, smem, &pre);
         return;
     }
     if (threadIdx.x >= 256) return;  // group 0 holds the sums; no barrier follows
@@ -1456,6 +1482,8 @@ __device__ __forceinline__ void gemm_q_k2_body(const VkfGemmArgs &a) {
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
+    // (no epilogue prefetch here: the 24 registers it holds through the main
+    // loop made these kernels 10-14 % slower on MI355X)
     gemm_mainloop_qdma_k2<QT>(a, r0, c0, acc, smem);
     epilogue_tile_k2(a, r0, c0, acc, smem);
 }
