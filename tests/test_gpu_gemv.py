@@ -204,7 +204,7 @@ def test_gemv_q6k_q81_dot(dev, N, K):
     assert rel_err(y, ref) <= TOL_F32
 
 
-MFMA_TYPES = [O.Q4_K, O.Q5_K, O.Q4_0, O.Q4_1, O.Q8_0]
+MFMA_TYPES = [O.Q4_K, O.Q5_K, O.Q4_0, O.Q4_1, O.Q8_0, O.Q5_0]
 
 
 @pytest.mark.parametrize("qt", MFMA_TYPES, ids=[O.QNAMES[q] for q in MFMA_TYPES])
@@ -212,7 +212,7 @@ MFMA_TYPES = [O.Q4_K, O.Q5_K, O.Q4_0, O.Q4_1, O.Q8_0]
 @pytest.mark.parametrize("N", [77, 3001])
 @pytest.mark.parametrize("K", [2304, 13824])
 def test_gemv_mfma(dev, qt, M, N, K):
-    """Q4_K, Q5_K, Q4_0, Q4_1, Q8_0 x fp16 at 2 <= M <= 16 on the matrix cores: 8- and
+    """Q4_K, Q5_K, Q4_0, Q4_1, Q8_0, Q5_0 x fp16 at 2 <= M <= 16 on the matrix cores: 8- and
     16-row activation images, every K-split width the host picks, and
     K = 13824, which runs as several K-slice launches accumulating into y."""
     from vkflame_amd import ops
@@ -237,7 +237,7 @@ def test_gemv_mfma_q6_k(dev, M, N, K):
     assert _per_row_err(y, x64, w, O.Q6_K, N, K) <= TOL_F32
 
 
-MFMA_ALL = [O.Q4_K, O.Q5_K, O.Q4_0, O.Q4_1, O.Q8_0, O.Q6_K]
+MFMA_ALL = [O.Q4_K, O.Q5_K, O.Q4_0, O.Q4_1, O.Q8_0, O.Q6_K, O.Q5_0]
 
 
 @pytest.mark.parametrize("qt", MFMA_ALL, ids=[O.QNAMES[q] for q in MFMA_ALL])

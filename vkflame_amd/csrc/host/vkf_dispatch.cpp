@@ -219,7 +219,7 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
         if (xk == 1 && (!aligned(x, 16) || (ldx % 4) != 0)) return kInval;
         VkfGemvArgs a{(const uint8_t *)w, x, y, row_bytes, (uint64_t)ldx, (uint64_t)ldy,
                       (uint32_t)M, (uint32_t)N, (uint32_t)K, 0u};
-        // Q4_K, Q4_0, Q4_1, Q6_K, Q5_K, Q8_0 at 2 <= M <= 16 on the matrix cores
+        // Q4_K, Q4_0, Q4_1, Q6_K, Q5_K, Q8_0, Q5_0 at 2 <= M <= 16 on the matrix cores
         // (fp32 and Q8_1 activations converted to the fp16 LDS image)
         // (kernels/gemv_mfma.hip; faster than the dot GEMV from M = 2 up,
         // e.g. Q4_0 11008x4096 M=4 13.2 vs 16.9 us on MI355X): the
@@ -233,6 +233,7 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
                        : qt == VKF_Q6_K ? 3
                        : qt == VKF_Q5_K ? 4
                        : qt == VKF_Q8_0 ? 5
+                       : qt == VKF_Q5_0 ? 6
                                         : -1;
         const bool kmin = mf == 0 || mf == 4;  // Q4_K / Q5_K: sub-block sums of x staged too
         // Q8_0 at M <= 4 stays on the dot GEMV unless N gives two tiles per CU
@@ -250,10 +251,10 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
             const uint32_t cus = (uint32_t)vkf::cu_count(), tiles = cdiv(N, 16);
             const uint32_t P = mfma_split(tiles, cus);
             const uint32_t G = 16 / P, grid = cdiv(tiles, G) < cus ? cdiv(tiles, G) : cus;
-            const uint64_t group_bytes = mf == 2 ? 160 : mf == 3 ? 210 : mf == 4 ? 176 : mf == 5 ? 272 : 144;
-            // kernel table: the six formats with fp16, then fp32, then Q8_1 activations
-            static_assert(VKF_K_GEMV_MFMA_Q8_0_Q81 == VKF_K_GEMV_MFMA_Q4_K_F16 + 17, "matrix-core GEMV table order");
-            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_MFMA_Q4_K_F16 + mf + 6 * xk);
+            const uint64_t group_bytes = mf == 2 ? 160 : mf == 3 ? 210 : (mf == 4 || mf == 6) ? 176 : mf == 5 ? 272 : 144;
+            // kernel table: the seven formats with fp16, then fp32, then Q8_1 activations
+            static_assert(VKF_K_GEMV_MFMA_Q5_0_Q81 == VKF_K_GEMV_MFMA_Q4_K_F16 + 20, "matrix-core GEMV table order");
+            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_MFMA_Q4_K_F16 + mf + 7 * xk);
             const uint64_t x_group_bytes = xk == 0 ? 512 : xk == 1 ? 1024 : 288;  // 256 k of one row
             for (uint32_t s0 = 0; s0 < nsb; s0 += per) {
                 const uint32_t n_sb = nsb - s0 < per ? nsb - s0 : per;

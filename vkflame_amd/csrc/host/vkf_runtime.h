@@ -72,18 +72,21 @@
     X(GEMV_MFMA_Q6_K_F16, "vkf_gemv_mfma_q6_k_f16")        \
     X(GEMV_MFMA_Q5_K_F16, "vkf_gemv_mfma_q5_k_f16")        \
     X(GEMV_MFMA_Q8_0_F16, "vkf_gemv_mfma_q8_0_f16")        \
+    X(GEMV_MFMA_Q5_0_F16, "vkf_gemv_mfma_q5_0_f16")         \
     X(GEMV_MFMA_Q4_K_F32, "vkf_gemv_mfma_q4_k_f32")         \
     X(GEMV_MFMA_Q4_0_F32, "vkf_gemv_mfma_q4_0_f32")         \
     X(GEMV_MFMA_Q4_1_F32, "vkf_gemv_mfma_q4_1_f32")         \
     X(GEMV_MFMA_Q6_K_F32, "vkf_gemv_mfma_q6_k_f32")         \
     X(GEMV_MFMA_Q5_K_F32, "vkf_gemv_mfma_q5_k_f32")         \
     X(GEMV_MFMA_Q8_0_F32, "vkf_gemv_mfma_q8_0_f32")         \
+    X(GEMV_MFMA_Q5_0_F32, "vkf_gemv_mfma_q5_0_f32")         \
     X(GEMV_MFMA_Q4_K_Q81, "vkf_gemv_mfma_q4_k_q8_1")        \
     X(GEMV_MFMA_Q4_0_Q81, "vkf_gemv_mfma_q4_0_q8_1")        \
     X(GEMV_MFMA_Q4_1_Q81, "vkf_gemv_mfma_q4_1_q8_1")        \
     X(GEMV_MFMA_Q6_K_Q81, "vkf_gemv_mfma_q6_k_q8_1")        \
     X(GEMV_MFMA_Q5_K_Q81, "vkf_gemv_mfma_q5_k_q8_1")        \
     X(GEMV_MFMA_Q8_0_Q81, "vkf_gemv_mfma_q8_0_q8_1")        \
+    X(GEMV_MFMA_Q5_0_Q81, "vkf_gemv_mfma_q5_0_q8_1")        \
     /* dot-product GEMV: per format {f16, f32} x {m1, m4} */ \
     X(GEMV_DOT_Q4_0_F16_M1, "vkf_gemv_dot_q4_0_f16_m1") \
     X(GEMV_DOT_Q4_0_F32_M1, "vkf_gemv_dot_q4_0_f32_m1") \

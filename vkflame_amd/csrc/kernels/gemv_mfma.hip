@@ -1,5 +1,5 @@
 // gemv_mfma.hip — small-batch GEMV (2 <= M <= 16) of Q4_K, Q5_K, Q4_0, Q4_1,
-// Q8_0 and Q6_K weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T,
+// Q5_0, Q8_0 and Q6_K weights on the matrix cores: y[M, N] = x[M, K] . Wdeq[N, K]^T,
 // with fp16, fp32 or Q8_1 activations (the latter two staged in LDS as
 // fp16: fp32 rounded once, Q8_1 as fp16(d*q), the value the prefill GEMM's
 // activation decode produces).
@@ -62,6 +62,8 @@
 //   8n + 4h + g.  Step t = 4n + 2h + hf takes elements x = 8hf .. +7.  Super-
 //   blocks (210 bytes) are 2-byte aligned: each run loads from the 4-byte
 //   aligned address below it and is shifted into place (v_alignbyte).
+//   Q5_0: the block pair 2g, 2g+1 (44 bytes: d, qh, qs of each), the same
+//   steps as Q4_0; element e's fifth bit is bit e of the block's qh.
 //   Q8_0: the block pair 2g, 2g+1 (68 bytes); step t = 4blk + s takes
 //   elements 8s .. +7 of block 2g + blk (the same k as Q4_0's steps).
 //   Q4_0 / Q4_1: the block pair 2g, 2g+1 of the group (36 or 40 contiguous
@@ -81,7 +83,7 @@
 #include "vkf_device.h"
 
 #define GM_WAVES 16
-enum { GF_Q4_K = 0, GF_Q4_0 = 1, GF_Q4_1 = 2, GF_Q6_K = 3, GF_Q5_K = 4, GF_Q8_0 = 5 };
+enum { GF_Q4_K = 0, GF_Q4_0 = 1, GF_Q4_1 = 2, GF_Q6_K = 3, GF_Q5_K = 4, GF_Q8_0 = 5, GF_Q5_0 = 6 };
 
 // formats with a per-sub-block min term (dmin * mn), fed by the sub-block sums of x
 template <int F> constexpr bool gm_kmin() { return F == GF_Q4_K || F == GF_Q5_K; }
@@ -99,7 +101,7 @@ template <int F> constexpr bool gm_pingpong() { return F != GF_Q5_K && F != GF_Q
 template <int F> constexpr int gm_half() { return gm_pingpong<F>() ? gm_maxsb<F>() / 2 : gm_maxsb<F>(); }
 
 template <int F> constexpr uint32_t gm_group_bytes() {
-    return F == GF_Q4_1 ? 160 : F == GF_Q6_K ? 210 : F == GF_Q5_K ? 176 : F == GF_Q8_0 ? 272 : 144;
+    return F == GF_Q4_1 ? 160 : F == GF_Q6_K ? 210 : (F == GF_Q5_K || F == GF_Q5_0) ? 176 : F == GF_Q8_0 ? 272 : 144;
 }
 
 // k offset, within its 256-k group, of the 8 elements of MFMA step t, k-slice g
@@ -271,6 +273,10 @@ struct GmSb {
     vkf_u4 v[3];
 };
 template <>
+struct GmSb<GF_Q5_0> {
+    vkf_u4 v[3];  // bytes 0 .. 15, 16 .. 31, 28 .. 43 of the block pair
+};
+template <>
 struct GmSb<GF_Q8_0> {
     vkf_u4 v[4];  // bytes 0 .. 63 of the block pair
     uint32_t e;   // bytes 64 .. 67
@@ -306,6 +312,11 @@ __device__ __forceinline__ void gm_load(const uint8_t *row, uint32_t sb, int g, 
             t.e[k] = *(const uint32_t *)(a + off[k] + (k < 4 || t.sh ? 16 : 12));
         }
         t.d = *(const uint16_t *)(b + 208);
+    } else if constexpr (F == GF_Q5_0) {
+        const uint8_t *p = b + 44 * g;
+        t.v[0] = *(const u4a4 *)p;
+        t.v[1] = *(const u4a4 *)(p + 16);
+        t.v[2] = *(const u4a4 *)(p + 28);
     } else if constexpr (F == GF_Q8_0) {
         const uint8_t *p = b + 68 * g;
 #pragma unroll
@@ -413,6 +424,33 @@ __device__ __forceinline__ vkf_h8 gm_decode_q8(uint32_t d0, uint32_t d1, vkf_h2 
 #pragma unroll
     for (int k = 0; k < 4; k++) r[k] = gm_u((gm_h2(p[k]) + m1152) * d2);
     return __builtin_bit_cast(vkf_h8, r);
+}
+
+// Q5_0: d*(q - 16) of 8 elements: code dwords d0, d1 (nibble HI), fifth bits
+// b0, b1 (bit 4k of byte... : bit k of the element's byte, one byte per
+// element, as gm_decode5 takes them); d2 = {d, d}
+template <int HI>
+__device__ __forceinline__ vkf_h8 gm_decode_q50(uint32_t d0, uint32_t d1, uint32_t b0, uint32_t b1, vkf_h2 d2,
+                                                uint32_t c64) {
+    vkf_h2 h[4];
+    gm_nibbles<HI>(d0, d0 >> 8, d1, d1 >> 8, c64, h);
+    const uint32_t m5 = HI ? 0x01000100u : 0x00100010u;
+    const uint32_t f[4] = {HI ? b0 << 8 : b0 << 4, HI ? b0 : b0 >> 4, HI ? b1 << 8 : b1 << 4, HI ? b1 : b1 >> 4};
+    // (1024 + q) - 1040 or (1024 + 16q)/16 - 80: q - 16, exact; then d, one rounding
+    const _Float16 sc = HI ? (_Float16)0.0625f : (_Float16)1.0f, of = HI ? (_Float16)-80.0f : (_Float16)-1040.0f;
+    const vkf_h2 sc2 = {sc, sc}, of2 = {of, of};
+    vkf_u4 r;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const vkf_h2 q = __builtin_elementwise_fma(gm_h2(gm_and_or(f[p], m5, gm_u(h[p]))), sc2, of2);
+        r[p] = gm_u(q * d2);
+    }
+    return __builtin_bit_cast(vkf_h8, r);
+}
+
+// the four fifth bits of elements e .. e+3 (bits e.. of qh) one per byte, at bit 0
+__device__ __forceinline__ uint32_t gm_spread4(uint32_t qh, uint32_t e) {
+    return (((qh >> e) & 0xfu) * 0x00204081u) & 0x01010101u;
 }
 
 // Q4_0 (d*(q - 8)) or Q4_1 (d*q + m) weights of 8 elements; d, m fp16
@@ -546,6 +584,38 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
                     const float d = vkf_h2f(T.d);
 #pragma unroll
                     for (int e = 0; e < 4; e++) y4[e] = fmaf(d, acc[e], y4[e]);
+                } else if constexpr (F == GF_Q5_0) {
+                    // block 0: d at bytes 0-1, qh 2 .. 5, qs 6 .. 21; block 1: d at 22-23,
+                    // qh 24 .. 27, qs 28 .. 43 (dwords w[k] = bytes 4k .. 4k+3)
+                    const GmSb<F> &T = tt[u];
+                    const uint32_t w[11] = {T.v[0][0], T.v[0][1], T.v[0][2], T.v[0][3], T.v[1][0], T.v[1][1],
+                                            T.v[1][2], T.v[1][3], T.v[2][1], T.v[2][2], T.v[2][3]};
+                    uint32_t q[2][4], qh[2], dd[2];
+                    dd[0] = w[0] & 0xffffu;
+                    qh[0] = __builtin_amdgcn_alignbyte(w[1], w[0], 2);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) q[0][k] = __builtin_amdgcn_alignbyte(w[k + 2], w[k + 1], 2);
+                    dd[1] = w[5] >> 16;
+                    qh[1] = w[6];
+                    q[1][0] = w[7]; q[1][1] = w[8]; q[1][2] = w[9]; q[1][3] = w[10];
+#pragma unroll
+                    for (int blk = 0; blk < 2; blk++) {
+                        const _Float16 d = gm_f16(dd[blk]);
+                        const vkf_h2 d2 = {d, d};
+#pragma unroll
+                        for (int hf = 0; hf < 2; hf++) {
+                            const uint32_t c0 = q[blk][2 * hf], c1 = q[blk][2 * hf + 1];
+                            // steps 4blk + hf (elements 8hf .. +7, low nibbles) and 4blk + 2 + hf (16 + 8hf .., high)
+                            const unsigned char *xp = xg + (4 * blk + hf) * (4 * MR * 16);
+                            const vkf_h8 xl = *(const vkf_h8 *)xp;
+                            const vkf_h8 xh = *(const vkf_h8 *)(xp + 2 * (4 * MR * 16));
+                            const uint32_t el = 8 * hf, eh = 16 + 8 * hf;
+                            const vkf_h8 bl = gm_decode_q50<0>(c0, c1, gm_spread4(qh[blk], el), gm_spread4(qh[blk], el + 4), d2, c64);
+                            const vkf_h8 bh = gm_decode_q50<1>(c0, c1, gm_spread4(qh[blk], eh), gm_spread4(qh[blk], eh + 4), d2, c64);
+                            y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, y4, 0, 0, 0);
+                            y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, y4, 0, 0, 0);
+                        }
+                    }
                 } else if constexpr (F == GF_Q8_0) {
                     // block 0: d at bytes 0-1, codes 2 .. 33; block 1: d at 34-35, codes 36 .. 67
                     const GmSb<F> &T = tt[u];
@@ -733,3 +803,4 @@ VKF_GEMV_MFMA(q4_1, GF_Q4_1)
 VKF_GEMV_MFMA(q6_k, GF_Q6_K)
 VKF_GEMV_MFMA(q5_k, GF_Q5_K)
 VKF_GEMV_MFMA(q8_0, GF_Q8_0)
+VKF_GEMV_MFMA(q5_0, GF_Q5_0)
