@@ -186,6 +186,46 @@ def test_gemv_dot_dynamic_range(dev, qt):
         assert rel_err(y[m], ref[m]) <= TOL_F32, m
 
 
+@pytest.mark.parametrize("qt", DOT_TYPES, ids=[O.QNAMES[q] for q in DOT_TYPES])
+@pytest.mark.parametrize("N", [77, 3001, 13824])
+@pytest.mark.parametrize("K", [1536, 5120, 16384])
+def test_gemv_dot_q8_1_m1(dev, qt, N, K):
+    """Q8_1 activations at M = 1 on the dot GEMV: each 8-element item staged
+    from its block as fp32 d*q (exact), then into the kernel's integer image
+    like fp32 activations; K = 16384 is the longest row the LDS image holds."""
+    from vkflame_amd import ops
+    w = O.gen_weight(qt, N, K, seed_for(2, 130 + qt))
+    xa, x64 = _x("q8_1", 1, K, seed_for(2, 131))
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
+    assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32
+
+
+@pytest.mark.parametrize("qt", DOT_TYPES, ids=[O.QNAMES[q] for q in DOT_TYPES])
+def test_gemv_dot_q8_1_m1_range(dev, qt):
+    """Q8_1 blocks whose scales span 12 decades (neighbouring blocks of one
+    64-element chunk share its exponent), d*q past fp16's range, all-zero
+    blocks and a row of a single non-zero code."""
+    from vkflame_amd import ops
+    N, K = 300, 4096
+    rng = np.random.default_rng(seed_for(2, 140 + qt))
+    w = O.gen_weight(qt, N, K, seed_for(2, 141 + qt))
+    for case in range(3):
+        x = rng.normal(0, 1, (1, K)).astype(np.float32)
+        if case == 0:
+            x[0] *= np.repeat(10.0 ** rng.uniform(-6, 6, K // 32), 32).astype(np.float32)
+        elif case == 1:
+            x[0] *= 1e5
+            x[0, 64:256] = 0.0
+        else:
+            x[0] = 0.0
+            x[0, 1001] = 7.25
+        xa = O.np_quantize_q8_1(x).reshape(1, -1)
+        x64 = O.np_dequant(O.Q8_1, xa).reshape(1, K).astype(np.float64)
+        y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
+        ref = O.ref_gemv(x64, O.np_dequant(qt, w).reshape(N, K))
+        assert rel_err(y[0], ref[0]) <= TOL_F32, case
+
+
 @pytest.mark.parametrize("N", [1, 77, 3001, 20011])
 @pytest.mark.parametrize("K", [2048, 4608, 5120, 6144])
 def test_gemv_q6k_q81_dot(dev, N, K):
@@ -300,7 +340,7 @@ def test_gemv_mfma_q6_k_extreme_scales(dev):
 
 
 @pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_1, O.Q4_K, O.Q5_K], ids=["q4_0", "q4_1", "q4_k", "q5_k"])
-@pytest.mark.parametrize("kind", ["f16", "f32"])
+@pytest.mark.parametrize("kind", ["f16", "f32", "q8_1"])
 @pytest.mark.parametrize("NK", [(77, 1600), (77, 1664), (77, 1728), (3001, 4096), (100003, 2624)],
                          ids=["77x1600", "77x1664", "77x1728", "3001x4096", "100003x2624"])
 def test_gemv_dot_lds_tails(dev, qt, kind, NK):

@@ -273,23 +273,27 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
         // into LDS by contiguous direct loads (kernels/gemv_dot.hip
         // gemv_dot_lds): two 3 KiB buffers per wave next to the activations
         const int li = qt == VKF_Q4_0 ? 0 : qt == VKF_Q4_1 ? 1 : qt == VKF_Q4_K ? 2 : qt == VKF_Q5_K ? 3 : -1;
-        if (li >= 0 && M == 1 && xk != 2 && (K % 64) == 0 && K <= kDotMaxK && kDotLdsL <= vkf::max_lds() &&
+        if (li >= 0 && M == 1 && (K % 64) == 0 && K <= kDotMaxK && kDotLdsL <= vkf::max_lds() &&
             aligned(w, kDotAlign[fi]) && (row_bytes % kDotAlign[fi]) == 0) {
             const uint32_t cus = (uint32_t)vkf::cu_count();
             const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 64), 1, cus * kDotWaves);
             const uint32_t tiles = cdiv(N, 64 / seg);
             a.flags |= seg << 8;
-            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_DOTL_Q4_0_F16 + 2 * li + xk);
+            // kernel table: per format fp16, fp32, Q8_1 activations
+            static_assert(VKF_K_GEMV_DOTL_Q5_K_Q81 == VKF_K_GEMV_DOTL_Q4_0_F16 + 11, "dot GEMV table order");
+            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_DOTL_Q4_0_F16 + 3 * li + xk);
             return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * kDotWaves), a, S(stream), kDotLdsL);
         }
         const size_t lds = M == 1 ? kDotLdsM1 : kDotLdsM4;
-        if (fi >= 0 && M <= 4 && xk != 2 && (K % 64) == 0 && K <= kDotMaxK && lds <= vkf::max_lds() &&
+        if (fi >= 0 && M <= 4 && (xk != 2 || (qt == VKF_Q8_0 && M == 1)) && (K % 64) == 0 && K <= kDotMaxK &&
+            lds <= vkf::max_lds() &&
             aligned(w, kDotAlign[fi]) && (row_bytes % kDotAlign[fi]) == 0) {
             const uint32_t rpl = M == 1 ? 1 : 2, cus = (uint32_t)vkf::cu_count();
             const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 64), rpl, cus * kDotWaves);
             const uint32_t tiles = cdiv(N, (64 / seg) * rpl);
             a.flags |= seg << 8;
-            const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_DOT_Q4_0_F16_M1 + 4 * fi + (M == 1 ? 0 : 2) + xk);
+            const VkfKernelId k = xk == 2 ? VKF_K_GEMV_DOT_Q8_0_Q81_M1
+                                          : (VkfKernelId)(VKF_K_GEMV_DOT_Q4_0_F16_M1 + 4 * fi + (M == 1 ? 0 : 2) + xk);
             return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * kDotWaves), a, S(stream), lds);
         }
         // Q6_K x Q8_1 at M = 1 (kernels/gemv_q6k.hip): 128-element chunks,

@@ -60,12 +60,16 @@
     X(GEMV_Q6K_F32_DOT_M1, "vkf_gemv_q6k_f32_dot_m1")      \
     X(GEMV_DOTL_Q4_0_F16, "vkf_gemv_dotl_q4_0_f16")        \
     X(GEMV_DOTL_Q4_0_F32, "vkf_gemv_dotl_q4_0_f32")        \
+    X(GEMV_DOTL_Q4_0_Q81, "vkf_gemv_dotl_q4_0_q8_1")       \
     X(GEMV_DOTL_Q4_1_F16, "vkf_gemv_dotl_q4_1_f16")        \
     X(GEMV_DOTL_Q4_1_F32, "vkf_gemv_dotl_q4_1_f32")        \
+    X(GEMV_DOTL_Q4_1_Q81, "vkf_gemv_dotl_q4_1_q8_1")       \
     X(GEMV_DOTL_Q4_K_F16, "vkf_gemv_dotl_q4_k_f16")        \
     X(GEMV_DOTL_Q4_K_F32, "vkf_gemv_dotl_q4_k_f32")        \
+    X(GEMV_DOTL_Q4_K_Q81, "vkf_gemv_dotl_q4_k_q8_1")       \
     X(GEMV_DOTL_Q5_K_F16, "vkf_gemv_dotl_q5_k_f16")        \
     X(GEMV_DOTL_Q5_K_F32, "vkf_gemv_dotl_q5_k_f32")        \
+    X(GEMV_DOTL_Q5_K_Q81, "vkf_gemv_dotl_q5_k_q8_1")       \
     X(GEMV_MFMA_Q4_K_F16, "vkf_gemv_mfma_q4_k_f16")        \
     X(GEMV_MFMA_Q4_0_F16, "vkf_gemv_mfma_q4_0_f16")        \
     X(GEMV_MFMA_Q4_1_F16, "vkf_gemv_mfma_q4_1_f16")        \
@@ -108,6 +112,7 @@
     X(GEMV_DOT_Q5_K_F32_M1, "vkf_gemv_dot_q5_k_f32_m1") \
     X(GEMV_DOT_Q5_K_F16_M4, "vkf_gemv_dot_q5_k_f16_m4") \
     X(GEMV_DOT_Q5_K_F32_M4, "vkf_gemv_dot_q5_k_f32_m4") \
+    X(GEMV_DOT_Q8_0_Q81_M1, "vkf_gemv_dot_q8_0_q8_1_m1") \
     X(GEMM_F16, "vkf_gemm_f16")                             \
     X(GEMM_I8, "vkf_gemm_i8")                               \
     X(GEMM_F16_K2, "vkf_gemm_f16_k2")                       \

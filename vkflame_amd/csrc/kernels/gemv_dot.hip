@@ -79,7 +79,14 @@ __device__ __forceinline__ void dot_load_x(const VkfGemvArgs &a, uint32_t i, uin
     if (i >= items) return;
     const uint32_t m = (i >= K8) + (i >= 2 * K8) + (i >= 3 * K8), r = i - m * K8;
     const uint64_t off = (uint64_t)m * a.ldx + 8ull * r;
-    if (XK == 1) {
+    if (XK == 2) {
+        // Q8_1 (ldx in bytes, 36-byte blocks of 32): d*q, exact in fp32
+        const uint8_t *b = (const uint8_t *)a.x + (uint64_t)m * a.ldx + 36ull * (r >> 2);
+        const float d = vkf_h2f(*(const uint16_t *)b);
+        const vkf_u2 q = *(const vkf_u2a4 *)(b + 4 + 8 * (r & 3));
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = d * (float)(int8_t)(q[j >> 2] >> (8 * (j & 3)));
+    } else if (XK == 1) {
         const vkf_f4 *p = (const vkf_f4 *)((const float *)a.x + off);
         const vkf_f4 p0 = p[0], p1 = p[1];
         v[0] = p0[0]; v[1] = p0[1]; v[2] = p0[2]; v[3] = p0[3];
@@ -654,14 +661,21 @@ VKF_GEMV_DOT(q4_1, VKF_Q4_1)
 VKF_GEMV_DOT(q8_0, VKF_Q8_0)
 VKF_GEMV_DOT(q4_k, VKF_Q4_K)
 VKF_GEMV_DOT(q5_k, VKF_Q5_K)
+// Q8_1 activations, M = 1 (the other formats take them through LDS below)
+VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dot_q8_0_q8_1_m1(VkfGemvArgs a) {
+    gemv_dot<VKF_Q8_0, 2, 1, 1, dot_depth<VKF_Q8_0>(1)>(a);
+}
 
-// M = 1 through LDS: vkf_gemv_dotl_{q4_0,q4_1,q4_k,q5_k}_{f16,f32}
+// M = 1 through LDS: vkf_gemv_dotl_{q4_0,q4_1,q4_k,q5_k}_{f16,f32,q8_1}
 #define VKF_GEMV_DOTL(name, QT)                                                                         \
     VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dotl_##name##_f16(VkfGemvArgs a) {       \
         gemv_dot_lds_entry<QT, 0>(a);                                                                   \
     }                                                                                                   \
     VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dotl_##name##_f32(VkfGemvArgs a) {       \
         gemv_dot_lds_entry<QT, 1>(a);                                                                   \
+    }                                                                                                   \
+    VKF_KERNEL void __launch_bounds__(64 * DOT_WAVES) vkf_gemv_dotl_##name##_q8_1(VkfGemvArgs a) {      \
+        gemv_dot_lds_entry<QT, 2>(a);                                                                   \
     }
 VKF_GEMV_DOTL(q4_0, VKF_Q4_0)
 VKF_GEMV_DOTL(q4_1, VKF_Q4_1)
