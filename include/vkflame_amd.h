@@ -103,9 +103,9 @@ int vkflame_quantize_rows_i8(const void *x, int x_dtype, int M, int K, int64_t l
  * the weight tile dequantised into LDS.  K % block_elems == 0.
  * With Q8_1 activations at M = 1, Q6_K weights use the exact integer dot
  * product (v_dot4_i32_i8), Q4_0, Q4_1, Q8_0, Q4_K and Q5_K the fp32 values
- * dx*q put on a 14-bit grid per 64 elements (as fp32 activations are), Q5_0
- * the exact fp32 values; at 2 <= M <= 16 the matrix-core GEMV (Q4_0, Q4_1,
- * Q8_0, Q5_0, Q4_K, Q5_K, Q6_K) and the GEMM take fp16(dx*q) (the GEMV after scaling each row
+ * dx*q put on a 14-bit grid per 64 elements (as fp32 activations are); at
+ * 2 <= M <= 16 the matrix-core GEMV (Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K; Q5_0
+ * from M = 1 when N gives two 16-row tiles per CU) and the GEMM take fp16(dx*q) (the GEMV after scaling each row
  * by a power of two, so no row overflows fp16), and fp32 activations on the
  * matrix-core GEMV are rounded to fp16 the same way.
  * This is the fused form of the reference's quant mul_mat path, which

@@ -280,6 +280,20 @@ def test_gemv_mfma_q6_k(dev, M, N, K):
 MFMA_ALL = [O.Q4_K, O.Q5_K, O.Q4_0, O.Q4_1, O.Q8_0, O.Q6_K, O.Q5_0]
 
 
+@pytest.mark.parametrize("kind", ["f16", "f32", "q8_1"])
+@pytest.mark.parametrize("N", [77, 3001, 20011])
+@pytest.mark.parametrize("K", [2304, 13824])
+def test_gemv_mfma_q5_0_m1(dev, kind, N, K):
+    """Q5_0 at M = 1: the generic GEMV below two 16-row tiles per CU, the
+    matrix-core GEMV above (N = 20011), whose staged rows past the first
+    repeat it and are not written."""
+    from vkflame_amd import ops
+    w = O.gen_weight(O.Q5_0, N, K, seed_for(2, 150))
+    xa, x64 = _x(kind, 1, K, seed_for(2, 151))
+    y = ops.gemm_q(to_dev(w, dev), O.Q5_0, to_dev(xa, dev), N, K).cpu().numpy()
+    assert _per_row_err(y, x64, w, O.Q5_0, N, K) <= TOL_F32
+
+
 @pytest.mark.parametrize("qt", MFMA_ALL, ids=[O.QNAMES[q] for q in MFMA_ALL])
 @pytest.mark.parametrize("kind", ["f32", "q8_1"])
 @pytest.mark.parametrize("M", [2, 9])
