@@ -132,6 +132,23 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int quant_type, uint64_t row_bytes
 /* Workspace bytes vkflame_dispatch_gemm_q_ws uses for these arguments (0: none). */
 size_t vkflame_gemm_q_workspace_bytes(int x_dtype, int M, int K);
 
+/* vkflame_dispatch_gemm_q that allocates nothing: the one scratch buffer of
+ * that entry point (the fp16 copy of Q8_1 activations at M > 16, M*K*2 bytes)
+ * is a fixed device array of VKFLAME_NOALLOC_SCRATCH_BYTES inside the library,
+ * one per GPU, held until the process ends.  No reference counterpart: it is
+ * for callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  Same arguments and
+ * results as vkflame_dispatch_gemm_q; returns hipErrorInvalidValue (and says
+ * so on stderr) when M*K*2 exceeds the array.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams, or
+ * threads) race and must be ordered by the caller.  The first call on a device
+ * looks the array up (hipGetSymbolAddress); make it outside graph capture. */
+#define VKFLAME_NOALLOC_SCRATCH_BYTES (16u << 20)
+int vkflame_dispatch_gemm_q_noalloc(const void *w, int quant_type, uint64_t row_bytes, const void *x, int x_dtype,
+                                    int64_t ldx, float *y, int64_t ldy, int M, int N, int K, void *stream);
+/* Size of that array in bytes (VKFLAME_NOALLOC_SCRATCH_BYTES). */
+size_t vkflame_noalloc_scratch_bytes(void);
+
 /* Integer partials of Q6_K weights w[N, K] x Q8_1 activations xq[M, K]:
  * P[(m*N + n)*(K/32) + kb] = sum over the 32 elements of block kb of
  * q8 * sc * (q6 - 32).  Exact int32; a test hook for the integer core of the

@@ -58,6 +58,9 @@ def lib() -> ctypes.CDLL:
     L.vkflame_dispatch_gemm_q_ws.argtypes = [P, I, U64, P, I, I64, P, I64, I, I, I, P, ctypes.c_size_t, P]
     L.vkflame_gemm_q_workspace_bytes.argtypes = [I, I, I]
     L.vkflame_gemm_q_workspace_bytes.restype = ctypes.c_size_t
+    L.vkflame_dispatch_gemm_q_noalloc.argtypes = [P, I, U64, P, I, I64, P, I64, I, I, I, P]
+    L.vkflame_noalloc_scratch_bytes.argtypes = []
+    L.vkflame_noalloc_scratch_bytes.restype = ctypes.c_size_t
     L.vkflame_q6_k_q8_1_partials.argtypes = [P, P, P, I, I, I, P]
     L.vkflame_stream_read.argtypes = [P, U64, P, P]
     L.vkflame_quantize_rows_i8.argtypes = [P, I, I, I, I64, P, P, P]
@@ -68,7 +71,7 @@ def lib() -> ctypes.CDLL:
                                          ctypes.POINTER(P), ctypes.POINTER(LaunchPlan)]
     L.vkflame_execute_launch.argtypes = [ctypes.POINTER(LaunchPlan), P]
     for f in ("vkflame_dispatch_dequant", "vkflame_quantize_q8_1", "vkflame_dispatch_gemm_q",
-              "vkflame_dispatch_gemm_q_ws",
+              "vkflame_dispatch_gemm_q_ws", "vkflame_dispatch_gemm_q_noalloc",
               "vkflame_q6_k_q8_1_partials", "vkflame_dispatch_linear", "vkflame_dispatch_linear_int8",
               "vkflame_stream_read", "vkflame_quantize_rows_i8",
               "vkflame_resolve_launch", "vkflame_execute_launch", "vkflame_init",
