@@ -5,7 +5,12 @@
  * Every entry point takes plain device pointers, sizes and a hipStream_t
  * (declared here as void* so the header needs no HIP include).  All work is
  * enqueued asynchronously on the given stream (0 = the legacy default
- * stream); nothing is allocated on the device and nothing synchronises.
+ * stream) and nothing synchronises.  One entry point allocates device memory:
+ * vkflame_dispatch_gemm_q takes a stream-ordered workspace (hipMallocAsync /
+ * hipFreeAsync) for Q8_1 activations at M > 16; callers that must not allocate
+ * use vkflame_dispatch_gemm_q_ws (their own workspace) or
+ * vkflame_dispatch_gemm_q_noalloc (the library's fixed array).  Every other
+ * entry point allocates nothing.
  * Return value: 0 on success, otherwise a hipError_t code
  * (1 = hipErrorInvalidValue for bad arguments, 98 = hipErrorInvalidDeviceFunction
  * on a device that is not gfx950, or the HIP error of a failed launch).
@@ -35,6 +40,7 @@ extern "C" {
 /* extra codes of this library (no reference counterpart) */
 #define VKF_DTYPE_INT32 10
 #define VKF_DTYPE_Q8_1 11  /* activations given as ggml Q8_1 blocks */
+#define VKF_DTYPE_INT8_INT32OUT 12  /* int8 x int8 -> raw int32 (exact) */
 
 /* quant type codes: runtime/dispatch.h:14-21 */
 #define VKF_DEQUANT_Q4_0 0
@@ -171,9 +177,22 @@ int vkflame_stream_read(const void *src, uint64_t bytes, uint32_t *sink, void *s
  *   op(B) = B[K,N] (transB = 0) or B stored [N,K] (transB = 1)
  * dtype VKF_DTYPE_FP16: A, B, C, D fp16, fp32 accumulation.
  * dtype VKF_DTYPE_FP16_FP32OUT: A, B fp16; C, D fp32.
- * dtype VKF_DTYPE_INT8: A, B int8, C, D int32, exact; activation must be 0;
- *   alpha/beta (int32*) as in hipblasGemmEx with HIPBLAS_COMPUTE_32I.
- * alpha/beta: host pointers to float (int32 for INT8), NULL = 1 and 0.
+ * dtype VKF_DTYPE_FP32: A, B, C, D fp32 (fp32 matrix cores; the reference
+ *   runs FP32 through its fp16 shader, runtime/dispatch.cpp:270-282).
+ * dtype VKF_DTYPE_INT8: the reference's int8 linear (kernels/linear_int8.glsl
+ *   :8-24, 60-100): A fp16, quantised in the kernel to
+ *   q = clamp(round_half_even(A / act_scale), -127, 127); B int8 weights;
+ *   act_scale = *alpha (float, NULL = 1; the reference's "caller may pass via
+ *   alpha", runtime/dispatch.cpp:302); C = per-output-channel w_scale, fp32
+ *   [N] (NULL = 1; the reference binds D in its place,
+ *   runtime/dispatch.cpp:305-308); beta NULL or 0;
+ *   D fp16 = f16(act(float(acc) * w_scale[n] * act_scale)), acc the exact
+ *   int32 sum (the reference omits act_scale here and only passes 1).
+ * dtype VKF_DTYPE_INT8_INT32OUT (no reference code): A, B int8, C, D int32,
+ *   exact; activation must be 0; alpha/beta (int32*) as in hipblasGemmEx with
+ *   HIPBLAS_COMPUTE_32I.
+ * alpha/beta: host pointers to float (int32 for INT8_INT32OUT), NULL = 1 and 0.
+ * VKF_DTYPE_BF16 returns hipErrorNotSupported.
  * C may be NULL when beta is 0.  Matrices are packed (ld = row length). */
 int vkflame_dispatch_linear(const void *A, const void *B, const void *C, void *D, int M, int N, int K, int dtype,
                             int transA, int transB, int activation, const void *alpha, const void *beta,

@@ -12,12 +12,18 @@
  * ignores ld, alpha, beta and the hipBLASLt epilogue inputs,
  * shim/hipblas_shim.cpp:282-287, shim/hipblaslt_shim.cpp:418-423):
  *   - hipblasGemmEx: column-major C = alpha*op(A)*op(B) + beta*C for every
- *     op combination and ld; (16F,16F -> 16F or 32F, compute 32F) and
- *     (8I,8I -> 32I, compute 32I, exact).
+ *     op combination and ld; (16F,16F -> 16F or 32F, compute 32F),
+ *     (32F,32F -> 32F, compute 32F) and (8I,8I -> 32I, compute 32I, exact).
+ *   - hipblasSgemm*: fp32 on the fp32 matrix cores.
  *   - hipblasLtMatmul: D = act(alpha*(A.B)*a_scale[m]*b_scale[n] + beta*C +
  *     bias) with BIAS, A/B_SCALE_POINTER (OUTER_VEC_32F vectors or scalars),
  *     RELU / GELU / SILU epilogues, row- or column-major layouts.
- * Unsupported type combinations return HIPBLAS_STATUS_NOT_SUPPORTED.
+ * With ROCm's hipBLAS / hipBLASLt present (and a GPU visible) the handles and
+ * descriptors these functions create are ROCm's own objects: functions not
+ * listed here reach ROCm with objects it created, and calls this library does
+ * not run (other types, device-pointer scalars, epilogues it lacks) are
+ * forwarded to ROCm's function of the same name.  Without ROCm's libraries
+ * such calls return HIPBLAS_STATUS_NOT_SUPPORTED.
  */
 #ifndef VKFLAME_AMD_BLAS_H
 #define VKFLAME_AMD_BLAS_H
@@ -39,6 +45,9 @@
     X(hipblasHgemm, "shim/hipblas_shim.cpp:116-143")                        \
     X(hipblasHgemmBatched, "shim/hipblas_shim.cpp:168-189")                \
     X(hipblasHgemmStridedBatched, "shim/hipblas_shim.cpp:219-249")         \
+    X(hipblasSgemm, "shim/hipblas_shim.cpp:84-113")                        \
+    X(hipblasSgemmBatched, "shim/hipblas_shim.cpp:145-166")                \
+    X(hipblasSgemmStridedBatched, "shim/hipblas_shim.cpp:191-217")         \
     X(hipblasLtCreate, "shim/hipblaslt_shim.cpp:104-110")                  \
     X(hipblasLtDestroy, "shim/hipblaslt_shim.cpp:112-116")                 \
     X(hipblasLtMatrixLayoutCreate, "shim/hipblaslt_shim.cpp:120-134")      \

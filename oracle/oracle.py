@@ -265,6 +265,30 @@ def np_quantize_rows_i8(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return q, scale
 
 
+def np_quantize_act_i8(x: np.ndarray, act_scale: float) -> np.ndarray:
+    """Activation quantisation of the reference's int8 linear
+    (kernels/linear_int8.glsl:63-70): q = clamp(round(x / act_scale), -127,
+    127) on fp16 activations, in float32 with an IEEE division.  GLSL's
+    round() leaves halves to the implementation; this build rounds them to
+    even (the GPU's v_rndne_f32)."""
+    x = np.asarray(x, dtype=np.float16).astype(F32)
+    return np.clip(np.rint((x / F32(act_scale)).astype(F32)), -127, 127).astype(np.int8)
+
+
+def ref_linear_int8_fp16a(A16: np.ndarray, W: np.ndarray, act_scale: float, w_scale, act: int = 0):
+    """The reference's int8 linear contract (kernels/linear_int8.glsl:48-101):
+    fp16 A quantised by act_scale, int8 W [N, K], exact int32 acc, then
+    act(f32(acc) * w_scale[n] * act_scale) (the reference omits act_scale
+    from the product and only ever passes 1).  Returns (acc int32, D float32
+    before the fp16 rounding)."""
+    q = np_quantize_act_i8(A16, act_scale)
+    acc = q.astype(np.int64) @ np.asarray(W, np.int64).T
+    assert np.abs(acc).max() < 2 ** 31
+    ws = np.ones(W.shape[0], F32) if w_scale is None else np.asarray(w_scale, F32)
+    y = (acc.astype(np.float64) * ws.astype(np.float64)[None, :] * float(act_scale)).astype(F32)
+    return acc.astype(np.int32), np_act(act, y)
+
+
 def np_act(act: int, x: np.ndarray) -> np.ndarray:
     """Activation epilogue in float32 (kernels/linear_fp16.glsl:22-36)."""
     x = x.astype(F32)

@@ -8,7 +8,8 @@ from vkflame_amd import lib
 P, I, U64, I64, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_int64, ctypes.c_size_t
 
 OP_N, OP_T, OP_C = 111, 112, 113
-R_32F, R_16F, R_8I, R_32I = 0, 2, 3, 10
+GEMM_DEFAULT = 160  # HIPBLAS_GEMM_DEFAULT
+R_32F, R_16F, R_8I, R_32I, R_16BF = 0, 2, 3, 10, 14
 COMPUTE_16F, COMPUTE_32F, COMPUTE_32I = 0, 2, 9
 ST_SUCCESS, ST_NOT_INIT, ST_INVALID_VALUE, ST_NOT_SUPPORTED, ST_HANDLE_NULL = 0, 1, 3, 7, 9
 
@@ -38,6 +39,11 @@ def blas():
     L.hipblasGemmStridedBatchedEx.argtypes = [P, I, I, I, I, I, P, P, I, I, I64, P, I, I, I64, P, P, I, I, I64,
                                               I, I, I]
     L.hipblasHgemm.argtypes = [P, I, I, I, I, I, P, P, I, P, I, P, P, I]
+    L.hipblasHgemmBatched.argtypes = [P, I, I, I, I, I, P, P, I, P, I, P, P, I, I]
+    L.hipblasSgemm.argtypes = [P, I, I, I, I, I, P, P, I, P, I, P, P, I]
+    L.hipblasSgemmBatched.argtypes = [P, I, I, I, I, I, P, P, I, P, I, P, P, I, I]
+    L.hipblasSgemmStridedBatched.argtypes = [P, I, I, I, I, I, P, P, I, I64, P, I, I64, P, P, I, I64, I]
+    L.hipblasGemmBatchedEx.argtypes = [P, I, I, I, I, I, P, P, I, I, P, I, I, P, P, I, I, I, I, I]
     L.hipblasLtCreate.argtypes = [ctypes.POINTER(P)]
     L.hipblasLtDestroy.argtypes = [P]
     L.hipblasLtMatrixLayoutCreate.argtypes = [ctypes.POINTER(P), I, U64, U64, I64]
@@ -72,3 +78,16 @@ def layout(L, dtype, rows, cols, ld, order=ORDER_COL):
         o = ctypes.c_int32(order)
         assert L.hipblasLtMatrixLayoutSetAttribute(h, LAYOUT_ORDER, ctypes.byref(o), 4) == 0
     return h
+
+
+def vendor_hipblas():
+    """ROCm's own hipBLAS (for calls this library does not export)."""
+    V = ctypes.CDLL("libhipblas.so")
+    V.hipblasSscal.argtypes = [P, I, P, P, I]
+    return V
+
+
+def vendor_hipblaslt():
+    V = ctypes.CDLL("libhipblaslt.so")
+    V.hipblasLtMatmulPreferenceGetAttribute.argtypes = [P, I, P, SZ, ctypes.POINTER(SZ)]
+    return V

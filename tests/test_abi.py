@@ -17,7 +17,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 HIPBLAS = ["hipblasCreate", "hipblasDestroy", "hipblasSetStream", "hipblasGetStream", "hipblasSetPointerMode",
            "hipblasGetPointerMode", "hipblasGemmEx", "hipblasGemmBatchedEx", "hipblasGemmStridedBatchedEx",
-           "hipblasHgemm", "hipblasHgemmBatched", "hipblasHgemmStridedBatched"]
+           "hipblasHgemm", "hipblasHgemmBatched", "hipblasHgemmStridedBatched", "hipblasSgemm",
+           "hipblasSgemmBatched", "hipblasSgemmStridedBatched"]
 HIPBLASLT = ["hipblasLtCreate", "hipblasLtDestroy", "hipblasLtMatrixLayoutCreate", "hipblasLtMatrixLayoutDestroy",
              "hipblasLtMatrixLayoutSetAttribute", "hipblasLtMatrixLayoutGetAttribute", "hipblasLtMatmulDescCreate",
              "hipblasLtMatmulDescDestroy", "hipblasLtMatmulDescSetAttribute", "hipblasLtMatmulDescGetAttribute",
@@ -60,8 +61,9 @@ def test_library_does_not_interpose_hip_runtime():
     assert not any(s.startswith("hipLaunch") or s.startswith("hipMalloc") for s in exp)
 
 
-def test_preload_exports_only_hiplaunchkernel():
-    assert _exported(VL.PRELOAD_PATH) == {"hipLaunchKernel"}
+def test_preload_exports_only_the_launch_entry_points():
+    assert _exported(VL.PRELOAD_PATH) == {"hipLaunchKernel", "hipModuleLaunchKernel", "hipExtModuleLaunchKernel",
+                                          "hipModuleGetFunction"}
 
 
 def test_version_and_block_geometry():
@@ -118,8 +120,8 @@ def test_table_mul_mat_before_dequant_substrings():
     p = VL.resolve_launch("mul_mat_q4_0_q8_1", (1, 1, 1), (64, 1, 1), args)
     assert (p.kind, p.quant_type, p.K, p.N, p.M) == (VL.LAUNCH_MUL_MAT_Q, 0, 4096, 11008, 7)
     assert (p.src, p.src1, p.dst) == (0x10, 0x20, 0x30)
-    for nm, qt in [("mul_mat_q4_1", 1), ("mul_mat_vec_q8_0", 2), ("mul_mat_q5_0", 3), ("mul_mat_q4_K", 4),
-                   ("mul_mat_q5_K", 5), ("mul_mat_q6_K", 6)]:
+    for nm, qt in [("mul_mat_q4_1_q8_1", 1), ("mul_mat_vec_q8_0_q8_1", 2), ("mul_mat_q5_0_q8_1", 3),
+                   ("mul_mat_q4_K_q8_1", 4), ("mul_mat_q5_K_q8_1", 5), ("mul_mat_q6_K_q8_1", 6)]:
         assert VL.resolve_launch(nm, (1, 1, 1), (64, 1, 1), args).quant_type == qt
     pf = VL.resolve_launch("mul_mat_f16", (1, 1, 1), (64, 1, 1), args)
     assert (pf.kind, pf.M, pf.N, pf.K) == (VL.LAUNCH_MUL_MAT_F16, 7, 11008, 4096)
@@ -132,7 +134,18 @@ def test_table_falls_through():
                "some_other_kernel", "mul_mat_bf16"]:
         assert VL.resolve_launch(nm, (1, 1, 1), (64, 1, 1), args).kind == VL.LAUNCH_NONE, nm
     bad = [P(1), P(2), P(3), ctypes.c_int32(0), ctypes.c_int32(5), ctypes.c_int32(6), ctypes.c_int32(7)]
-    assert VL.resolve_launch("mul_mat_q4_0", (1, 1, 1), (64, 1, 1), bad).kind == VL.LAUNCH_NONE
+    assert VL.resolve_launch("mul_mat_q4_0_q8_1", (1, 1, 1), (64, 1, 1), bad).kind == VL.LAUNCH_NONE
+
+
+def test_table_mul_mat_without_q8_1_falls_through():
+    """Quantised mul_mat kernels that do not take Q8_1 activations (ggml's
+    dequantize_mul_mat_vec: 5 arguments, fp32 y, the weight type in its
+    template arguments) keep their own kernel: the table does not read a
+    7-argument layout they do not have."""
+    args = [P(1), P(2), P(3), ctypes.c_int32(4096), ctypes.c_int32(4096)]
+    for nm in ["_Z22dequantize_mul_mat_vecILi32ELi2EXadL_ZL15dequantize_q4_0PKvllR6float2EEEvS1_PKfPfii",
+               "dequantize_mul_mat_vec_q4_K", "mul_mat_q4_0", "mul_mat_vec_q6_K_f32"]:
+        assert VL.resolve_launch(nm, (1, 1, 1), (64, 1, 1), args).kind == VL.LAUNCH_NONE, nm
 
 
 # ---------------------------------------------------------------------------
@@ -157,8 +170,19 @@ def test_c_abi_rejects_bad_arguments():
     assert L.vkflame_dispatch_gemm_q(P(16), 4, 0, P(16), 1, 0, P(16), 0, 0, 8, 256, s) == 0   # M = 0: no-op
     assert L.vkflame_dispatch_gemm_q(P(16), 4, 0, P(16), 0, 0, P(16), 0, 32, 8, 256, s) == 801  # fp32 prefill
     assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 1, 0, 0, 7, None, None, s) == 1
-    assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 0, 0, 0, 0, None, None, s) == 801
-    assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 2, 0, 1, 1, None, None, s) == 1
+    assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 3, 0, 0, 0, None, None, s) == 801  # bf16
+    half = ctypes.c_float(0.5)
+    assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 0, 0, 0, 0, None, ctypes.byref(half),
+                                     s) == 1  # fp32 with beta != 0 and no C
+    assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 12, 0, 1, 1, None, None, s) == 1
+    # the reference int8 contract: act_scale (alpha) must be finite and > 0, beta 0
+    for bad_scale in (0.0, -1.0, float("inf"), float("nan")):
+        f = ctypes.c_float(bad_scale)
+        assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 2, 0, 1, 0, ctypes.byref(f), None,
+                                         s) == 1
+    one, half = ctypes.c_float(1.0), ctypes.c_float(0.5)
+    assert L.vkflame_dispatch_linear(P(16), P(16), None, P(16), 4, 4, 4, 2, 0, 1, 0, ctypes.byref(one),
+                                     ctypes.byref(half), s) == 1
     assert L.vkflame_dispatch_linear_int8(P(16), None, P(16), None, None, 1, P(16), 2, 4, 4, 4, 0, s) == 1
     assert L.vkflame_q6_k_q8_1_partials(P(16), P(16), P(16), 1, 1, 100, s) == 1
     assert L.vkflame_stream_read(P(16), 17, P(16), s) == 1                    # bytes % 16
@@ -190,13 +214,13 @@ def test_hipblas_handles_and_errors():
     one = ctypes.c_float(1.0)
     # NULL handle, bad op, bad ld, unsupported type pair: all rejected before a launch
     args = (B.OP_T, B.OP_N, 8, 8, 8, ctypes.byref(one), P(16), B.R_16F, 8, P(16), B.R_16F, 8, ctypes.byref(one),
-            P(16), B.R_32F, 8, B.COMPUTE_32F, 0)
+            P(16), B.R_32F, 8, B.COMPUTE_32F, B.GEMM_DEFAULT)
     assert L.hipblasGemmEx(None, *args) == B.ST_NOT_INIT
     assert L.hipblasGemmEx(h, 7, *args[1:]) == 10                                  # INVALID_ENUM
     bad_ld = list(args); bad_ld[8] = 4
     assert L.hipblasGemmEx(h, *bad_ld) == B.ST_INVALID_VALUE
-    f32 = list(args); f32[7] = B.R_32F; f32[10] = B.R_32F
-    assert L.hipblasGemmEx(h, *f32) == B.ST_NOT_SUPPORTED
+    bf16 = list(args); bf16[7] = 14; bf16[10] = 14                                # HIP_R_16BF
+    assert L.hipblasGemmEx(h, *bf16) == B.ST_NOT_SUPPORTED  # no vendor hipBLAS to forward to without a GPU
     empty = list(args); empty[2] = 0
     assert L.hipblasGemmEx(h, *empty) == B.ST_SUCCESS
     assert L.hipblasDestroy(h) == 0
@@ -253,4 +277,30 @@ def test_hipblaslt_descriptors_round_trip():
         assert L.hipblasLtMatrixLayoutDestroy(x) == 0
     assert L.hipblasLtMatmulDescDestroy(d) == 0
     assert L.hipblasLtMatmulPreferenceDestroy(pref) == 0
+    assert L.hipblasLtDestroy(h) == 0
+
+
+def test_hipblaslt_int32_out_needs_integral_scalars():
+    """int8 x int8 -> int32 scales by integers: a float alpha or beta that is
+    not an exact int32 (0.5, 1.5, 2^31) is refused before any launch (without
+    ROCm's hipBLASLt to forward to, as here); integral ones pass the check."""
+    L = B.blas()
+    h = ctypes.c_void_p()
+    assert L.hipblasLtCreate(ctypes.byref(h)) == 0
+    a = B.layout(L, B.R_8I, 64, 32, 64)
+    b = B.layout(L, B.R_8I, 64, 16, 64)
+    dd = B.layout(L, B.R_32I, 32, 16, 32)
+    d = ctypes.c_void_p()
+    assert L.hipblasLtMatmulDescCreate(ctypes.byref(d), B.COMPUTE_32I, B.R_32F) == 0
+    assert B.set_desc(L, d, B.DESC_TRANSA, B.OP_T) == 0
+    zero = ctypes.c_float(0.0)
+    for bad in (0.5, 1.5, -2.25, 2.0 ** 31):
+        al = ctypes.c_float(bad)
+        assert L.hipblasLtMatmul(h, d, ctypes.byref(al), P(16), a, P(16), b, ctypes.byref(zero), P(16), dd, P(16),
+                                 dd, None, None, 0, None) == B.ST_NOT_SUPPORTED, bad
+        assert L.hipblasLtMatmul(h, d, ctypes.byref(zero), P(16), a, P(16), b, ctypes.byref(al), P(16), dd, P(16),
+                                 dd, None, None, 0, None) == B.ST_NOT_SUPPORTED, bad
+    for x in (a, b, dd):
+        assert L.hipblasLtMatrixLayoutDestroy(x) == 0
+    assert L.hipblasLtMatmulDescDestroy(d) == 0
     assert L.hipblasLtDestroy(h) == 0

@@ -60,7 +60,7 @@ def test_gemm_ex_fp16(dev, L, handle, opA, opB, ctype):
         be = ctypes.c_uint16(int(np.float16(-0.5).view(np.uint16)))
         comp = B.COMPUTE_16F
     st = L.hipblasGemmEx(handle, opA, opB, m, n, k, ctypes.byref(al), _ptr(tA), B.R_16F, lda, _ptr(tB), B.R_16F,
-                         ldb, ctypes.byref(be), _ptr(tC), ctype, ldc, comp, 0)
+                         ldb, ctypes.byref(be), _ptr(tC), ctype, ldc, comp, B.GEMM_DEFAULT)
     assert st == B.ST_SUCCESS
     torch.cuda.synchronize()
     got = tC.cpu().numpy()
@@ -80,7 +80,7 @@ def test_gemm_ex_int8_int32(dev, L, handle):
     C = torch.zeros((n, m), dtype=torch.int32, device=dev)
     al, be = ctypes.c_int32(1), ctypes.c_int32(0)
     st = L.hipblasGemmEx(handle, B.OP_T, B.OP_N, m, n, k, ctypes.byref(al), _ptr(tA), B.R_8I, k, _ptr(tB),
-                         B.R_8I, k, ctypes.byref(be), _ptr(C), B.R_32I, m, B.COMPUTE_32I, 0)
+                         B.R_8I, k, ctypes.byref(be), _ptr(C), B.R_32I, m, B.COMPUTE_32I, B.GEMM_DEFAULT)
     assert st == B.ST_SUCCESS
     torch.cuda.synchronize()
     ref = (A.astype(np.int64) @ Bm.astype(np.int64))
@@ -100,7 +100,7 @@ def test_gemm_strided_batched_int8(dev, L, handle):
     al, be = ctypes.c_int32(2), ctypes.c_int32(0)
     st = L.hipblasGemmStridedBatchedEx(handle, B.OP_T, B.OP_N, m, n, k, ctypes.byref(al), _ptr(tA), B.R_8I, k,
                                        m * k, _ptr(tB), B.R_8I, k, n * k, ctypes.byref(be), _ptr(C), B.R_32I, m,
-                                       n * m, nb, B.COMPUTE_32I, 0)
+                                       n * m, nb, B.COMPUTE_32I, B.GEMM_DEFAULT)
     assert st == B.ST_SUCCESS
     torch.cuda.synchronize()
     for b in range(nb):
@@ -209,3 +209,203 @@ def test_launch_table_executes_dequant(dev):
     torch.cuda.synchronize()
     ref = O.c_dequant(O.Q4_K, w, out_f16=True)
     assert np.array_equal(dst.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+def _colmajor_dev(M, ld, dev, dtype):
+    """Upload the column-major matrix M (rows x cols) with leading dimension
+    ld: column j at offset j*ld."""
+    buf = np.zeros((M.shape[1], ld), dtype)
+    buf[:, :M.shape[0]] = M.T
+    return to_dev(buf, dev)
+
+
+@pytest.mark.parametrize("opA,opB", [(B.OP_T, B.OP_N), (B.OP_N, B.OP_N), (B.OP_N, B.OP_T), (B.OP_T, B.OP_T)])
+def test_sgemm(dev, L, handle, opA, opB):
+    """hipblasSgemm on the fp32 matrix cores: every op combination, padded ld,
+    alpha and beta (shim/hipblas_shim.cpp:84-113 ignores ld, alpha, beta)."""
+    import torch
+    m, n, k = 133, 77, 300
+    rng = np.random.default_rng(seed_for(4, 140) + opA + 3 * opB)
+    opa = rng.normal(0, 1, (m, k)).astype(np.float32)
+    opb = rng.normal(0, 1, (k, n)).astype(np.float32)
+    A = opa if opA == B.OP_N else opa.T
+    Bm = opb if opB == B.OP_N else opb.T
+    lda, ldb, ldc = A.shape[0] + 1, Bm.shape[0] + 4, m + 3
+    C0 = rng.normal(0, 1, (m, n)).astype(np.float32)
+    tA, tB = _colmajor_dev(A, lda, dev, np.float32), _colmajor_dev(Bm, ldb, dev, np.float32)
+    tC = _colmajor_dev(C0, ldc, dev, np.float32)
+    al, be = ctypes.c_float(1.25), ctypes.c_float(-0.75)
+    assert L.hipblasSgemm(handle, opA, opB, m, n, k, ctypes.byref(al), _ptr(tA), lda, _ptr(tB), ldb,
+                          ctypes.byref(be), _ptr(tC), ldc) == B.ST_SUCCESS
+    torch.cuda.synchronize()
+    got = tC.cpu().numpy()
+    ref = 1.25 * (opa.astype(np.float64) @ opb.astype(np.float64)) - 0.75 * C0.astype(np.float64)
+    assert rel_err(got[:, :m].T, ref) <= 1e-5
+    assert np.all(got[:, m:] == 0)                    # ld padding untouched
+
+
+def test_gemm_ex_fp32_and_linear_fp32(dev, L, handle):
+    """fp32 through hipblasGemmEx (32F, compute 32F) and
+    vkflame_dispatch_linear(VKF_DTYPE_FP32), row-major, C and beta."""
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_FP32
+    m, n, k = 256, 384, 512
+    rng = np.random.default_rng(seed_for(4, 141))
+    a = rng.normal(0, 1, (m, k)).astype(np.float32)
+    b = rng.normal(0, 1, (n, k)).astype(np.float32)
+    c = rng.normal(0, 1, (m, n)).astype(np.float32)
+    D = ops.linear(to_dev(a, dev), to_dev(b, dev), m, n, k, DTYPE_FP32, transB=1, C=to_dev(c, dev), alpha=0.5,
+                   beta=2.0)
+    torch.cuda.synchronize()
+    ref = 0.5 * (a.astype(np.float64) @ b.astype(np.float64).T) + 2.0 * c
+    assert rel_err(D.cpu().numpy(), ref) <= 1e-5
+    # column-major C^T[n, m] = b . a^T: opA = T on b stored [n,k] row-major = col-major k x n
+    Ct = torch.zeros((m, n), dtype=torch.float32, device=dev)
+    one, zero = ctypes.c_float(1.0), ctypes.c_float(0.0)
+    assert L.hipblasGemmEx(handle, B.OP_T, B.OP_N, n, m, k, ctypes.byref(one), _ptr(to_dev(b, dev)), B.R_32F, k,
+                           _ptr(to_dev(a, dev)), B.R_32F, k, ctypes.byref(zero), _ptr(Ct), B.R_32F, n,
+                           B.COMPUTE_32F, B.GEMM_DEFAULT) == B.ST_SUCCESS
+    torch.cuda.synchronize()
+    assert rel_err(Ct.cpu().numpy(), a.astype(np.float64) @ b.astype(np.float64).T) <= 1e-5
+
+
+def test_sgemm_strided_and_batched_one_launch(dev, L, handle):
+    """Strided and pointer-array batches (the arrays of device pointers live
+    in device memory, as hipBLAS defines them) run as one launch each and
+    match per-matrix products."""
+    import torch
+    m, n, k, nb = 96, 64, 160, 5
+    rng = np.random.default_rng(seed_for(4, 142))
+    A = rng.normal(0, 1, (nb, k, m)).astype(np.float32)   # column-major m x k (opA = N): column j = A[b, j]
+    Bm = rng.normal(0, 1, (nb, n, k)).astype(np.float32)  # column-major k x n
+    tA, tB = to_dev(A, dev), to_dev(Bm, dev)
+    C = torch.zeros((nb, n, m), dtype=torch.float32, device=dev)
+    al, be = ctypes.c_float(1.0), ctypes.c_float(0.0)
+    assert L.hipblasSgemmStridedBatched(handle, B.OP_N, B.OP_N, m, n, k, ctypes.byref(al), _ptr(tA), m, k * m,
+                                        _ptr(tB), k, n * k, ctypes.byref(be), _ptr(C), m, n * m, nb) == B.ST_SUCCESS
+    C2 = torch.zeros_like(C)
+    pa = torch.tensor([tA[b].data_ptr() for b in range(nb)], dtype=torch.int64, device=dev)
+    pb = torch.tensor([tB[b].data_ptr() for b in range(nb)], dtype=torch.int64, device=dev)
+    pc = torch.tensor([C2[b].data_ptr() for b in range(nb)], dtype=torch.int64, device=dev)
+    assert L.hipblasSgemmBatched(handle, B.OP_N, B.OP_N, m, n, k, ctypes.byref(al), _ptr(pa), m, _ptr(pb), k,
+                                 ctypes.byref(be), _ptr(pc), m, nb) == B.ST_SUCCESS
+    torch.cuda.synchronize()
+    for b in range(nb):
+        ref = A[b].T.astype(np.float64) @ Bm[b].T.astype(np.float64)   # (m x k) @ (k x n)
+        assert rel_err(C[b].cpu().numpy().T, ref) <= 1e-5
+        assert rel_err(C2[b].cpu().numpy().T, ref) <= 1e-5
+
+
+def test_hgemm_batched_device_pointer_arrays(dev, L, handle):
+    import torch
+    m, n, k, nb = 128, 128, 256, 3
+    rng = np.random.default_rng(seed_for(4, 143))
+    A = rng.normal(0, 1, (nb, m, k)).astype(np.float16)   # opA = T: stored col-major k x m = row-major m x k
+    Bm = rng.normal(0, 1, (nb, n, k)).astype(np.float16)  # opB = N: col-major k x n
+    tA, tB = to_dev(A, dev), to_dev(Bm, dev)
+    C = torch.zeros((nb, n, m), dtype=torch.float16, device=dev)
+    pa = torch.tensor([tA[b].data_ptr() for b in range(nb)], dtype=torch.int64, device=dev)
+    pb = torch.tensor([tB[b].data_ptr() for b in range(nb)], dtype=torch.int64, device=dev)
+    pc = torch.tensor([C[b].data_ptr() for b in range(nb)], dtype=torch.int64, device=dev)
+    one = ctypes.c_uint16(int(np.float16(1.0).view(np.uint16)))
+    zero = ctypes.c_uint16(0)
+    assert L.hipblasHgemmBatched(handle, B.OP_T, B.OP_N, m, n, k, ctypes.byref(one), _ptr(pa), k, _ptr(pb), k,
+                                 ctypes.byref(zero), _ptr(pc), m, nb) == B.ST_SUCCESS
+    torch.cuda.synchronize()
+    for b in range(nb):
+        ref = A[b].astype(np.float64) @ Bm[b].astype(np.float64).T
+        assert rel_err(C[b].cpu().numpy().T.astype(np.float32), ref) <= TOL_F16
+
+
+def test_gemm_ex_bf16_forwarded_to_rocm(dev, L, handle):
+    """A type pair this library does not run (bf16) is forwarded to ROCm's
+    hipblasGemmEx with the same (ROCm-created) handle and succeeds."""
+    import torch
+    m, n, k = 64, 48, 128
+    a = torch.randn(m, k, device=dev).to(torch.bfloat16)   # opA = T: col-major k x m (lda = k) = row-major m x k
+    b = torch.randn(n, k, device=dev).to(torch.bfloat16)   # opB = N: col-major k x n (ldb = k) = row-major n x k
+    c = torch.zeros(n, m, device=dev, dtype=torch.bfloat16)  # col-major m x n (ldc = m)
+    one, zero = ctypes.c_float(1.0), ctypes.c_float(0.0)
+    assert L.hipblasGemmEx(handle, B.OP_T, B.OP_N, m, n, k, ctypes.byref(one), _ptr(a), B.R_16BF, k, _ptr(b),
+                           B.R_16BF, k, ctypes.byref(zero), _ptr(c), B.R_16BF, m, B.COMPUTE_32F, B.GEMM_DEFAULT) == B.ST_SUCCESS
+    torch.cuda.synchronize()
+    ref = a.float().cpu().numpy().astype(np.float64) @ b.float().cpu().numpy().T.astype(np.float64)
+    assert rel_err(c.float().cpu().numpy().T, ref) <= TOL_F16
+
+
+def test_handle_works_with_rocm_functions(dev, L, handle):
+    """The handle hipblasCreate returns is ROCm's own: a hipBLAS function this
+    library does not export (hipblasSscal) runs on it."""
+    import torch
+    V = B.vendor_hipblas()
+    x = torch.arange(100, dtype=torch.float32, device=dev)
+    a = ctypes.c_float(3.0)
+    assert V.hipblasSscal(handle, 100, ctypes.byref(a), _ptr(x), 1) == B.ST_SUCCESS
+    torch.cuda.synchronize()
+    assert np.array_equal(x.cpu().numpy(), 3.0 * np.arange(100, dtype=np.float32))
+
+
+def test_lt_forwarded_and_rocm_objects(dev, L):
+    """hipBLASLt: a bf16 matmul (not run here) is forwarded to ROCm's
+    hipblasLtMatmul on ROCm-created objects, and a function this library does
+    not export (hipblasLtMatmulPreferenceGetAttribute) works on its
+    preference object."""
+    import torch
+    V = B.vendor_hipblaslt()
+    pref = ctypes.c_void_p()
+    assert L.hipblasLtMatmulPreferenceCreate(ctypes.byref(pref)) == 0
+    ws = ctypes.c_uint64(1 << 20)
+    assert L.hipblasLtMatmulPreferenceSetAttribute(pref, B.PREF_MAX_WORKSPACE, ctypes.byref(ws), 8) == 0
+    got = ctypes.c_uint64(0)
+    n_w = ctypes.c_size_t(0)
+    assert V.hipblasLtMatmulPreferenceGetAttribute(pref, B.PREF_MAX_WORKSPACE, ctypes.byref(got), 8,
+                                                   ctypes.byref(n_w)) == 0 and got.value == 1 << 20
+    L.hipblasLtMatmulPreferenceDestroy(pref)
+    m, n, k = 64, 32, 96
+    a = torch.randn(m, k, device=dev).to(torch.bfloat16)   # opA = T: col-major k x m = row-major m x k
+    b = torch.randn(n, k, device=dev).to(torch.bfloat16)   # col-major k x n = row-major n x k
+    d = torch.zeros(n, m, device=dev, dtype=torch.bfloat16)
+    adesc = B.layout(L, B.R_16BF, k, m, k)
+    bdesc = B.layout(L, B.R_16BF, k, n, k)
+    ddesc = B.layout(L, B.R_16BF, m, n, m)
+    desc = ctypes.c_void_p()
+    assert L.hipblasLtMatmulDescCreate(ctypes.byref(desc), B.COMPUTE_32F, B.R_32F) == 0
+    assert B.set_desc(L, desc, B.DESC_TRANSA, B.OP_T) == 0
+    st = _lt_matmul(L, dev, a, adesc, b, bdesc, d, ddesc, desc)
+    assert st == B.ST_SUCCESS
+    ref = a.float().cpu().numpy().astype(np.float64) @ b.float().cpu().numpy().T.astype(np.float64)
+    assert rel_err(d.float().cpu().numpy().T, ref) <= TOL_F16
+    for h in (adesc, bdesc, ddesc):
+        L.hipblasLtMatrixLayoutDestroy(h)
+    L.hipblasLtMatmulDescDestroy(desc)
+
+
+def test_lt_batched_one_launch_and_int32_alpha(dev, L):
+    """A strided batch of int8 -> int32 products with an integer alpha of 3
+    (scale type 32F), one launch for the batch, exact."""
+    import torch
+    m, n, k, nb = 128, 96, 256, 4
+    rng = np.random.default_rng(seed_for(4, 144))
+    A = rng.integers(-127, 128, (nb, m, k)).astype(np.int8)   # opA = T: col-major k x m
+    Bm = rng.integers(-127, 128, (nb, n, k)).astype(np.int8)  # col-major k x n
+    tA, tB = to_dev(A, dev), to_dev(Bm, dev)
+    D = torch.zeros((nb, n, m), dtype=torch.int32, device=dev)
+    adesc = B.layout(L, B.R_8I, k, m, k)
+    bdesc = B.layout(L, B.R_8I, k, n, k)
+    ddesc = B.layout(L, B.R_32I, m, n, m)
+    for h, stride in ((adesc, m * k), (bdesc, n * k), (ddesc, n * m)):
+        cnt, st_ = ctypes.c_int32(nb), ctypes.c_int64(stride)
+        assert L.hipblasLtMatrixLayoutSetAttribute(h, B.LAYOUT_BATCH_COUNT, ctypes.byref(cnt), 4) == 0
+        assert L.hipblasLtMatrixLayoutSetAttribute(h, B.LAYOUT_STRIDE, ctypes.byref(st_), 8) == 0
+    desc = ctypes.c_void_p()
+    assert L.hipblasLtMatmulDescCreate(ctypes.byref(desc), B.COMPUTE_32I, B.R_32F) == 0
+    assert B.set_desc(L, desc, B.DESC_TRANSA, B.OP_T) == 0
+    st = _lt_matmul(L, dev, tA, adesc, tB, bdesc, D, ddesc, desc, alpha=3.0)
+    assert st == B.ST_SUCCESS
+    for b in range(nb):
+        ref = 3 * (A[b].astype(np.int64) @ Bm[b].astype(np.int64).T)
+        assert np.array_equal(D[b].cpu().numpy().T.astype(np.int64), ref)
+    for h in (adesc, bdesc, ddesc):
+        L.hipblasLtMatrixLayoutDestroy(h)
+    L.hipblasLtMatmulDescDestroy(desc)

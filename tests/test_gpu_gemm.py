@@ -51,14 +51,49 @@ def test_linear_fp16_epilogue(dev, act):
 def test_linear_int8_int32_exact(dev, M, N, K):
     import torch
     from vkflame_amd import ops
-    from vkflame_amd._lib import DTYPE_INT8
+    from vkflame_amd._lib import DTYPE_INT8_INT32OUT
     rng = np.random.default_rng(seed_for(4, 60) + M)
     A = rng.integers(-127, 128, (M, K)).astype(np.int8)
     W = rng.integers(-127, 128, (N, K)).astype(np.int8)
-    D = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8, transB=1)
+    D = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8_INT32OUT, transB=1)
     torch.cuda.synchronize()
     ref = (A.astype(np.float64) @ W.astype(np.float64).T).astype(np.int64)  # exact: |sum| < 2^53
     assert np.array_equal(D.cpu().numpy().astype(np.int64), ref)
+
+
+@pytest.mark.parametrize("M,N,K,transA,transB,act", [(64, 96, 256, 0, 1, 0), (130, 70, 200, 0, 1, 1),
+                                                     (512, 640, 5120, 0, 1, 2), (100, 72, 384, 1, 0, 3),
+                                                     (33, 300, 1000, 1, 1, 0), (300, 128, 640, 0, 0, 2)])
+def test_linear_int8_reference_contract(dev, M, N, K, transA, transB, act):
+    """vkflame_dispatch_linear(VKF_DTYPE_INT8) as kernels/linear_int8.glsl
+    defines it: fp16 A quantised in the kernel by act_scale (alpha), int8
+    weights, per-channel w_scale (C), activation, fp16 D -- against the
+    oracle's exact int32 core and float64 epilogue."""
+    import ctypes
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_INT8
+    rng = np.random.default_rng(seed_for(4, 90) + M + K + act)
+    act_scale = 0.0371
+    A = (rng.normal(0, 1.5, (M, K))).astype(np.float16)
+    W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    ws = np.abs(rng.normal(0, 0.01, N)).astype(np.float32)
+    Am = A.T.copy() if transA else A
+    Wm = W if transB else W.T.copy()
+    D = ops.linear(to_dev(Am, dev), to_dev(Wm, dev), M, N, K, DTYPE_INT8, transA=transA, transB=transB, act=act,
+                   C=to_dev(ws, dev), alpha=act_scale)
+    torch.cuda.synchronize()
+    assert D.dtype == torch.float16
+    acc, y = O.ref_linear_int8_fp16a(A, W, act_scale, ws, act)
+    assert rel_err(D.cpu().numpy().astype(np.float32), y) <= TOL_F16
+    # act_scale 1 and integer-valued fp16 A: the int8 product itself, scaled
+    Ai = rng.integers(-127, 128, (M, K)).astype(np.float16)
+    Aim = Ai.T.copy() if transA else Ai
+    D1 = ops.linear(to_dev(Aim, dev), to_dev(Wm, dev), M, N, K, DTYPE_INT8, transA=transA, transB=transB,
+                    C=to_dev(ws, dev))
+    torch.cuda.synchronize()
+    ref = (Ai.astype(np.float64) @ W.astype(np.float64).T) * ws.astype(np.float64)[None, :]
+    assert rel_err(D1.cpu().numpy().astype(np.float32), ref) <= TOL_F16
 
 
 def _dense_shapes():
@@ -79,7 +114,7 @@ def _dense_shapes():
 def test_linear_dense_split_k_and_plain(dev):
     import torch
     from vkflame_amd import ops
-    from vkflame_amd._lib import DTYPE_FP16_FP32OUT, DTYPE_INT8
+    from vkflame_amd._lib import DTYPE_FP16_FP32OUT, DTYPE_INT8_INT32OUT
     small, big, cus = _dense_shapes()
     for (M, N, K) in small + big:
         tiles = -(-M // 128) * -(-N // 128)
@@ -87,7 +122,7 @@ def test_linear_dense_split_k_and_plain(dev):
         rng = np.random.default_rng(seed_for(4, 80) + M + N + K)
         A = rng.integers(-127, 128, (M, K)).astype(np.int8)
         W = rng.integers(-127, 128, (N, K)).astype(np.int8)
-        D = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8, transB=1)
+        D = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8_INT32OUT, transB=1)
         torch.cuda.synchronize()
         ref = A.astype(np.int64) @ W.astype(np.int64).T
         got = D.cpu().numpy().astype(np.int64)
@@ -119,12 +154,12 @@ def test_config4_linear_int8(dev):
     scales, fp16 bias, fp16 out."""
     import torch
     from vkflame_amd import ops
-    from vkflame_amd._lib import DTYPE_INT8
+    from vkflame_amd._lib import DTYPE_INT8_INT32OUT
     M = 512
     N = K = 5120
     inp = O.gen_int8_linear(M, N, K, seed_for(4))
     A, W = to_dev(inp.A, dev), to_dev(inp.W, dev)
-    acc = ops.linear(A, W, M, N, K, DTYPE_INT8, transB=1)
+    acc = ops.linear(A, W, M, N, K, DTYPE_INT8_INT32OUT, transB=1)
     D = ops.linear_int8(A, to_dev(inp.a_scale, dev), W, to_dev(inp.w_scale, dev), to_dev(inp.bias, dev))
     torch.cuda.synchronize()
     ref_acc = (inp.A.astype(np.float64) @ inp.W.astype(np.float64).T)
@@ -213,8 +248,11 @@ def test_config3_q4_k_prefill(dev):
 
 
 def test_config5_q6_k_q8_1_prefill(dev):
-    """C5 at M=512 on a 4096-row slice of the vocab projection (same kernel
-    and per-row work as the full 152064 rows)."""
+    """C5's activations (M = 512, K = 5120, Q8_1) on a 4096-row slice of the
+    vocab projection.  The slice is 128 tiles of 128 x 128, at most one per
+    CU, so it runs the split-K kernel (vkf_gemm_q6_k_f16_k2) after the
+    one-time activation decode; the full 152064 rows run the 256-row wide
+    kernel (test_config5_q6_k_q8_1_prefill_full)."""
     import torch
     from vkflame_amd import ops
     N, K, M = 4096, 5120, 512
@@ -294,3 +332,81 @@ def test_gemm_q_q8_1_workspace_paths(dev, qt, M, K):
     ref = O.ref_gemv(x64, O.np_dequant(qt, w).reshape(N, K))
     for y in (a, b, c):
         assert rel_err(y, ref) <= TOL_F32
+
+
+def _wide_route(M, N, cus):
+    """The dispatcher's condition for the 256-row wide kernel
+    (vkf_gemm_<q>_f16_w): fp16 (or workspace-decoded Q8_1) activations,
+    M >= 256, the wide grid filling at least half the CUs and the 128-row grid
+    more than one tile per CU."""
+    t = -(-N // 128)
+    return M >= 256 and 2 * t * -(-M // 256) >= cus and t * -(-M // 128) > cus
+
+
+def _split_k_route(M, N, cus):
+    """The condition for the split-K kernel (vkf_gemm_<q>_f16_k2): not wide
+    and the 128-row grid at most one tile per CU."""
+    return not _wide_route(M, N, cus) and -(-N // 128) * -(-M // 128) <= cus
+
+
+def test_config5_q6_k_q8_1_prefill_full(dev):
+    """C5 at its full size: Q6_K 152064 x 5120 weights x Q8_1 activations
+    [512, 5120] quantised on the GPU, through the route bench.py times: the
+    activations decoded once into a workspace, then the wide 256-row kernel
+    (vkf_gemm_q6_k_f16_w).  All 512 activation rows against the oracle's
+    float64 product on 1026 weight rows (first, last and a random sample)."""
+    import torch
+    from vkflame_amd import ops
+    N, K, M = 152064, 5120, 512
+    assert _wide_route(M, N, torch.cuda.get_device_properties(0).multi_processor_count)
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(5))
+    x = np.random.default_rng(seed_for(5, 1)).normal(0, 1, (M, K)).astype(np.float32)
+    wd = to_dev(w, dev)
+    xq = ops.quantize_q8_1(to_dev(x, dev))
+    rows = np.concatenate([[0, N - 1], np.random.default_rng(5).choice(N, 1024, replace=False)])
+    y = ops.gemm_q(wd, O.Q6_K, xq, N, K)
+    torch.cuda.synchronize()
+    ys = y[:, torch.from_numpy(rows).to(dev)].cpu().numpy()
+    del y, wd
+    torch.cuda.empty_cache()
+    xq_ref = O.np_quantize_q8_1(x).reshape(M, -1)
+    assert np.array_equal(xq.cpu().numpy(), xq_ref)
+    x64 = O.np_dequant(O.Q8_1, xq_ref).reshape(M, K).astype(np.float64)
+    wdq = O.np_dequant(O.Q6_K, w[rows]).reshape(len(rows), K)
+    assert rel_err(ys, O.ref_gemv(x64, wdq)) <= TOL_F32
+
+
+def test_wide_q6_k_q8_1_k5120(dev):
+    """The wide kernel at C5's K with Q8_1 activations decoded into the
+    workspace, every output checked: N = 8448 (66 tiles of 128 rows) is the
+    smallest multiple of 128 that takes the wide route at M = 512 on a
+    256-CU MI355X."""
+    import torch
+    from vkflame_amd import ops
+    N, K, M = 8448, 5120, 512
+    assert _wide_route(M, N, torch.cuda.get_device_properties(0).multi_processor_count)
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(5, 30))
+    x = np.random.default_rng(seed_for(5, 31)).normal(0, 1, (M, K)).astype(np.float32)
+    xq = O.np_quantize_q8_1(x).reshape(M, -1)
+    y = ops.gemm_q(to_dev(w, dev), O.Q6_K, to_dev(xq, dev), N, K)
+    torch.cuda.synchronize()
+    x64 = O.np_dequant(O.Q8_1, xq).reshape(M, K).astype(np.float64)
+    assert rel_err(y.cpu().numpy(), O.ref_gemv(x64, O.np_dequant(O.Q6_K, w).reshape(N, K))) <= TOL_F32
+
+
+def test_config3_q4_k_prefill_5120x13824(dev):
+    """C3's second shape at M = 512: Q4_K 5120 x 13824 (the down projection),
+    fp16 activations.  40 x 4 = 160 tiles of 128 x 128 on a 256-CU MI355X:
+    the split-K kernel (vkf_gemm_q4_k_f16_k2), the route bench.py times.  All
+    512 activation rows against the oracle on 514 weight rows."""
+    import torch
+    from vkflame_amd import ops
+    N, K, M = 5120, 13824, 512
+    assert _split_k_route(M, N, torch.cuda.get_device_properties(0).multi_processor_count)
+    w = O.gen_weight(O.Q4_K, N, K, seed_for(3, 5))
+    x = _f16(np.random.default_rng(seed_for(3, 517)), M, K)
+    y = ops.gemm_q(to_dev(w, dev), O.Q4_K, to_dev(x, dev), N, K).cpu().numpy()
+    torch.cuda.synchronize()
+    rows = np.concatenate([[0, N - 1], np.random.default_rng(6).choice(N, 512, replace=False)])
+    wd = O.np_dequant(O.Q4_K, w[rows]).reshape(len(rows), K)
+    assert rel_err(y[:, rows], O.ref_gemv(x.astype(np.float64), wd)) <= TOL_F32

@@ -32,10 +32,10 @@ def test_dequant_fixtures(dev, fx, qt):
 def test_q8_1_and_int_fixtures(dev, fx):
     import torch
     from vkflame_amd import ops
-    from vkflame_amd._lib import DTYPE_INT8
+    from vkflame_amd._lib import DTYPE_INT8_INT32OUT
     q = ops.quantize_q8_1(to_dev(fx["quant_x"], dev))
     A, B = fx["i8_A"], fx["i8_B"]
-    C = ops.linear(to_dev(A, dev), to_dev(B, dev), A.shape[0], B.shape[0], A.shape[1], DTYPE_INT8, transB=1)
+    C = ops.linear(to_dev(A, dev), to_dev(B, dev), A.shape[0], B.shape[0], A.shape[1], DTYPE_INT8_INT32OUT, transB=1)
     P = ops.q6k_q81_partials(to_dev(fx["q6k_w"], dev), to_dev(fx["q6k_xq"], dev), 3, 6, 512)
     torch.cuda.synchronize()
     assert np.array_equal(q.cpu().numpy(), fx["quant_blocks"])

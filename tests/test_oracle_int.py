@@ -49,3 +49,41 @@ def test_activation_epilogue():
         # A&S 7.1.26 erf is within 1.5e-7 of erf: GELU within ~1e-6 of the exact form
         assert abs(O.c_act(3, v) - 0.5 * v * (1 + math.erf(v / math.sqrt(2)))) <= 2e-6 * max(1, abs(v))
         assert abs(float(O.np_act(3, np.array([v], np.float32))[0]) - O.c_act(3, v)) <= 1e-6 * max(1, abs(v))
+
+
+def test_act_i8_quantiser_known_answers():
+    """kernels/linear_int8.glsl:63-70 worked by hand: q = clamp(round(x /
+    act_scale), -127, 127), halves to even, in float32."""
+    x = np.array([0.0, 1.0, -1.0, 2.5, 3.5, -2.5, -0.5, 0.49, 126.6, 200.0, -300.0, 65504.0], np.float16)
+    assert O.np_quantize_act_i8(x, 1.0).tolist() == [0, 1, -1, 2, 4, -2, 0, 0, 127, 127, -127, 127]
+    # act_scale 0.25: x / 0.25 exact (a power of two), 0.125 -> 0.5 -> 0, 0.375 -> 1.5 -> 2
+    y = np.array([0.125, 0.375, -0.375, 1.0, 31.75, 32.0], np.float16)
+    assert O.np_quantize_act_i8(y, 0.25).tolist() == [0, 2, -2, 4, 127, 127]
+
+
+def test_act_i8_quantiser_identity_and_row_rule():
+    """With act_scale = 1, integer-valued fp16 activations in [-127, 127] pass
+    through unchanged (the reference's only act_scale); with each row's own
+    max|x|/127 it is the per-row quantiser (tools/quantise.py:35-41)."""
+    rng = np.random.default_rng(11)
+    a = rng.integers(-127, 128, (7, 300)).astype(np.float16)
+    assert np.array_equal(O.np_quantize_act_i8(a, 1.0), a.astype(np.int8))
+    x = (rng.normal(0, 2, (5, 256))).astype(np.float16)
+    q_rows, s_rows = O.np_quantize_rows_i8(x.astype(np.float32))
+    for m in range(5):
+        assert np.array_equal(O.np_quantize_act_i8(x[m], float(s_rows[m])), q_rows[m])
+
+
+def test_ref_linear_int8_fp16a_exact_core():
+    """The reference contract's int32 core equals the int64 product of the
+    quantised operands; with act_scale 1 and integer A it is A . W^T."""
+    rng = np.random.default_rng(12)
+    A = rng.integers(-127, 128, (9, 160)).astype(np.float16)
+    W = rng.integers(-127, 128, (11, 160)).astype(np.int8)
+    acc, y = O.ref_linear_int8_fp16a(A, W, 1.0, None)
+    assert np.array_equal(acc, A.astype(np.int64) @ W.astype(np.int64).T)
+    assert np.array_equal(y, acc.astype(np.float32))
+    ws = np.abs(rng.normal(0, 0.01, 11)).astype(np.float32)
+    acc2, y2 = O.ref_linear_int8_fp16a(A * np.float16(0.5), W, 0.5, ws)
+    assert np.array_equal(acc2, acc)  # (A/2) / 0.5 = A exactly
+    assert np.allclose(y2, acc * ws[None, :] * 0.5, rtol=1e-6)

@@ -16,7 +16,7 @@ PRELOAD_PATH = os.path.join(HERE, "libvkflame_preload.so")
 
 # codes (include/vkflame_amd.h)
 DTYPE_FP32, DTYPE_FP16, DTYPE_INT8, DTYPE_BF16, DTYPE_FP16_FP32OUT = 0, 1, 2, 3, 4
-DTYPE_INT32, DTYPE_Q8_1 = 10, 11
+DTYPE_INT32, DTYPE_Q8_1, DTYPE_INT8_INT32OUT = 10, 11, 12
 Q4_0, Q4_1, Q8_0, Q5_0, Q4_K, Q5_K, Q6_K, Q8_1 = range(8)
 ACT_NONE, ACT_SILU, ACT_RELU, ACT_GELU_ERF = range(4)
 LAUNCH_NONE, LAUNCH_DEQUANT, LAUNCH_MUL_MAT_Q, LAUNCH_MUL_MAT_F16 = range(4)

@@ -419,15 +419,43 @@ int vkflame_dispatch_linear(const void *A, const void *B, const void *C, void *D
         if (dtype == VKF_DTYPE_FP16_FP32OUT) g.flags |= VKF_GF_D_F32 | VKF_GF_CIN_F32;
         return vkf::launch_gemm(VKF_K_GEMM_F16, g, S(stream));
     }
-    if (dtype == VKF_DTYPE_INT8) {
-        if (activation != 0) return kInval;
-        g.alpha = alpha ? (float)*(const int32_t *)alpha : 1.0f;
-        g.beta = beta ? (float)*(const int32_t *)beta : 0.0f;
+    if (dtype == VKF_DTYPE_FP32) {
+        // fp32 operands on the fp32 matrix cores (the reference sends FP32 to
+        // its fp16 shader, runtime/dispatch.cpp:270-282)
+        g.alpha = alpha ? *(const float *)alpha : 1.0f;
+        g.beta = beta ? *(const float *)beta : 0.0f;
         if (g.beta != 0.0f && !C) return kInval;
+        g.flags |= VKF_GF_D_F32 | VKF_GF_CIN_F32;
+        return vkf::launch_gemm(VKF_K_GEMM_F32, g, S(stream));
+    }
+    if (dtype == VKF_DTYPE_INT8) {
+        // kernels/linear_int8.glsl: fp16 A quantised in the kernel by
+        // act_scale (passed through alpha, runtime/dispatch.cpp:302), int8
+        // weights, per-output-channel w_scale (C here; the reference binds D
+        // in its place, runtime/dispatch.cpp:305-308), fp16 D with the
+        // activation.  D = f16(act(acc * w_scale[n] * act_scale)): the
+        // reference leaves act_scale out of the product (it only ever passes
+        // 1), this build dequantises both operands.
+        const float act_scale = alpha ? *(const float *)alpha : 1.0f;
+        if (!(act_scale > 0.0f) || act_scale == __builtin_inff()) return kInval;
+        if (beta && *(const float *)beta != 0.0f) return kInval;
+        g.Cin = nullptr;
+        g.cs = (const float *)C;
+        g.alpha = act_scale;
+        g.beta = 0.0f;
+        g.xscale = act_scale;
+        g.flags |= VKF_GF_X_F16Q;
+        return vkf::launch_gemm(VKF_K_GEMM_I8, g, S(stream));
+    }
+    if (dtype == VKF_DTYPE_INT8_INT32OUT) {
+        if (activation != 0) return kInval;
+        const int32_t ia = alpha ? *(const int32_t *)alpha : 1, ib = beta ? *(const int32_t *)beta : 0;
+        if (ib != 0 && !C) return kInval;
+        vkf_gemm_set_int_scalars(g, ia, ib);
         g.flags |= VKF_GF_D_I32;
         return vkf::launch_gemm(VKF_K_GEMM_I8, g, S(stream));
     }
-    return kNotSup;  // FP32 and BF16 GEMM are outside this library's path
+    return kNotSup;  // BF16 GEMM is outside this library's path
 }
 
 int vkflame_dispatch_linear_int8(const int8_t *A, const float *a_scale, const int8_t *W, const float *w_scale,

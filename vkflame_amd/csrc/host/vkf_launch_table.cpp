@@ -21,6 +21,8 @@
 //  * unknown and unsupported names (IQ formats) run the original kernel
 //    instead of returning hipSuccess without doing the work;
 //  * a bf16 mul_mat (whose name also contains "f16") is not taken for fp16;
+//  * a quantised mul_mat is routed only when its name also names the Q8_1
+//    activations its argument layout assumes;
 //  * fp16 mul_mat computes D[M,N] = vy[M,K] . vx[N,K]^T into the fp32 ggml
 //    destination (the reference passed vx as the M-row operand and wrote fp16).
 #include <cstdint>
@@ -71,7 +73,12 @@ int vkflame_resolve_launch(const char *name, unsigned grid_x, unsigned grid_y, u
         if (n.has("iq2") || n.has("iq3") || n.has("iq4")) return VKF_LAUNCH_NONE;
         bool quant = n.has("q4_0") || n.has("q4_1") || n.has("q4_K") || n.has("q5_0") || n.has("q5_K") ||
                      n.has("q6_K") || n.has("q8_0");
-        if (quant) {
+        // Only the quantised-weight x Q8_1-activation kernels the reference
+        // describes (mul_mat_q*_q8_1, shim/hip_runtime_shim.cpp:1097-1099)
+        // take this argument layout; other mul_mat kernels that name a weight
+        // type (ggml's dequantize_mul_mat_vec: 5 arguments, fp32 y) run as
+        // launched.
+        if (quant && n.has("q8_1")) {
             // (vx, vy, dst, ncols_x, nrows_x, ncols_y, nrows_y, ...) (1123-1125)
             plan->kind = VKF_LAUNCH_MUL_MAT_Q;
             plan->quant_type = mul_mat_qtype(n);

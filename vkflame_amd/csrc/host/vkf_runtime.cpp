@@ -8,6 +8,8 @@
 // a device needs them, and launched asynchronously on the caller's stream.
 #include "vkf_runtime.h"
 
+#include <dlfcn.h>
+
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -34,6 +36,21 @@ const char *const k_names[VKF_K_COUNT] = {
 };
 
 constexpr int kMaxDevices = 64;
+
+using ModuleLaunchFn = hipError_t (*)(hipFunction_t, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned,
+                                      unsigned, hipStream_t, void **, void **);
+using ModuleGetFunctionFn = hipError_t (*)(hipFunction_t *, hipModule_t, const char *);
+
+ModuleLaunchFn real_module_launch() {
+    static const ModuleLaunchFn fn = reinterpret_cast<ModuleLaunchFn>(real_hip_symbol("hipModuleLaunchKernel"));
+    return fn;
+}
+
+ModuleGetFunctionFn real_module_get_function() {
+    static const ModuleGetFunctionFn fn =
+        reinterpret_cast<ModuleGetFunctionFn>(real_hip_symbol("hipModuleGetFunction"));
+    return fn;
+}
 
 struct DeviceTable {
     std::once_flag once;
@@ -71,7 +88,7 @@ void load_device(DeviceTable &t, int dev) {
     for (int k = 0; k < VKF_K_COUNT; k++) {
         hipFunction_t f = nullptr;
         for (int i = 0; i < nm && !f; i++) {
-            if (hipModuleGetFunction(&f, mods[i], k_names[k]) != hipSuccess) f = nullptr;
+            if (real_module_get_function()(&f, mods[i], k_names[k]) != hipSuccess) f = nullptr;
         }
         if (!f) {
             std::fprintf(stderr, "[vkflame] kernel %s missing from the code objects\n", k_names[k]);
@@ -98,6 +115,15 @@ DeviceTable *table_for_current(hipError_t *err) {
 }
 
 }  // namespace
+
+void *real_hip_symbol(const char *name) {
+    static void *const runtime = [] () -> void * {
+        Dl_info info{};
+        if (!dladdr(reinterpret_cast<void *>(&hipGetDevice), &info) || !info.dli_fname) return nullptr;
+        return dlopen(info.dli_fname, RTLD_NOW | RTLD_NOLOAD);
+    }();
+    return runtime ? dlsym(runtime, name) : nullptr;
+}
 
 const char *kernel_name(VkfKernelId id) { return (id >= 0 && id < VKF_K_COUNT) ? k_names[id] : "?"; }
 
@@ -132,8 +158,9 @@ hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const void *args, size_
         debug_log("launch %s grid=(%u,%u,%u) block=(%u,%u,%u) lds=%zu stream=%p", k_names[id], grid.x, grid.y,
                   grid.z, block.x, block.y, block.z, shmem, (void *)stream);
     void *params[1] = {const_cast<void *>(args)};
-    return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, (unsigned)shmem, stream,
-                                 params, nullptr);
+    const ModuleLaunchFn real = real_module_launch();
+    if (!real) return hipErrorNotInitialized;
+    return real(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, (unsigned)shmem, stream, params, nullptr);
 }
 
 // The condition under which the dense GEMM kernels take their direct-to-LDS
@@ -143,11 +170,15 @@ static bool dma_operand(const void *p, uint64_t ld, bool trans, uint32_t K, uint
     return !trans && (ld * es) % 16 == 0 && ((uintptr_t)p & 15) == 0 && ((uint64_t)K * es) % 128 == 0;
 }
 
-hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream) {
-    if (g.R == 0 || g.Cn == 0) return hipSuccess;
-    dim3 grid((g.Cn + 127) / 128, (g.R + 127) / 128);
-    if (grid.y > 65535) return hipErrorInvalidValue;
-    if ((id == VKF_K_GEMM_F16 || id == VKF_K_GEMM_I8) && (uint64_t)grid.x * grid.y <= (uint64_t)cu_count()) {
+hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream, uint32_t batch) {
+    if (g.R == 0 || g.Cn == 0 || batch == 0) return hipSuccess;
+    dim3 grid((g.Cn + 127) / 128, (g.R + 127) / 128, batch);
+    if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
+    // the split-K kernels need operands the direct-to-LDS loads take, checked
+    // here on the host: not for per-batch pointer arrays, which live on the device
+    if ((id == VKF_K_GEMM_F16 || id == VKF_K_GEMM_I8) && !(g.flags & VKF_GF_X_F16Q) && !g.bpx &&
+        (uint64_t)grid.x * grid.y * batch <= (uint64_t)cu_count() &&
+        (batch == 1 || ((g.bsx | g.bsy) & 15) == 0)) {
         const uint32_t es = id == VKF_K_GEMM_F16 ? 2 : 1;
         if (dma_operand(g.X, g.ldx, (g.flags & VKF_GF_X_TRANS) != 0, g.K, es) &&
             dma_operand(g.Y, g.ldy, (g.flags & VKF_GF_Y_TRANS) != 0, g.K, es))

@@ -114,6 +114,7 @@
     X(GEMV_DOT_Q5_K_F32_M4, "vkf_gemv_dot_q5_k_f32_m4") \
     X(GEMV_DOT_Q8_0_Q81_M1, "vkf_gemv_dot_q8_0_q8_1_m1") \
     X(GEMM_F16, "vkf_gemm_f16")                             \
+    X(GEMM_F32, "vkf_gemm_f32")                             \
     X(GEMM_I8, "vkf_gemm_i8")                               \
     X(GEMM_F16_K2, "vkf_gemm_f16_k2")                       \
     X(GEMM_I8_K2, "vkf_gemm_i8_k2")                         \
@@ -171,14 +172,29 @@ inline hipError_t launch(VkfKernelId id, dim3 grid, dim3 block, const T &args, h
     return launch(id, grid, block, &args, sizeof(T), stream, shmem);
 }
 
-// A VkfGemmArgs launch: 128x128 output tile per 256-thread workgroup.  For
+// A VkfGemmArgs launch: 128x128 output tile per 256-thread workgroup, `batch`
+// matrices along grid z (g's batch strides or pointer arrays).  For
 // GEMM_F16 / GEMM_I8 with no more tiles than CUs and operands the
 // direct-to-LDS loads take, the 512-thread split-K kernel (_K2) instead.
-hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream);
+hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream, uint32_t batch = 1);
 
 // VKFLAME_DEBUG=1: one stderr line per dispatch (reference: torch_backend/mode.py:13).
 bool debug_enabled();
 void debug_log(const char *fmt, ...);
+
+// The HIP runtime's own definition of entry point `name` (looked up in the
+// shared object that defines hipGetDevice), never an interposer of the same
+// name: the library's own launches go straight to the runtime even when
+// libvkflame_preload.so, which interposes hipModuleLaunchKernel, is loaded.
+void *real_hip_symbol(const char *name);
+
+// The vendor library's (ROCm's) own definition of `name` in `lib`
+// ("libhipblas.so", "libhipblaslt.so"): the process's copy of that library
+// (dlopen'ed if it is not loaded yet) searched with dlsym on its handle, so
+// never this library's export of the same name.  nullptr when no GPU is
+// visible (the vendor libraries may end the process when they find none), or
+// the library or symbol is absent.
+void *vendor_symbol(const char *lib, const char *name);
 
 // Number of compute units of the current device (cached per device).
 int cu_count();

@@ -96,7 +96,16 @@ struct VkfGemmArgs {
     uint32_t act;
     float alpha, beta;
     uint32_t flags;        // VKF_GF_* below
-    uint32_t pad;
+    float xscale;          // VKF_GF_X_F16Q: the activation quantisation scale
+    // Batched launches of the dense kernels (vkf_gemm_f16 / _f32 / _i8 and
+    // their _k2 forms): matrix b = blockIdx.z sits at X + b*bsx, Y + b*bsy,
+    // D + b*bsd, Cin + b*bsc (byte strides), or, when bpx is set, at the
+    // device pointer arrays bpx[b], bpy[b], bpd[b] with Cin = D (hipBLAS's
+    // batched form).  Zero / null for one matrix.
+    uint64_t bsx, bsy, bsd, bsc;
+    const void *const *bpx;
+    const void *const *bpy;
+    void *const *bpd;
 };
 
 // VkfGemmArgs.flags
@@ -107,15 +116,25 @@ struct VkfGemmArgs {
 #define VKF_GF_Y_TRANS  16u   // Y stored [K, C] (element (c,k) at Y + k*ldy + c)
 #define VKF_GF_BIAS_ROW 32u   // bias indexed by r (length R) instead of c
 #define VKF_GF_D_I32    64u   // int8 kernel: store the raw int32 accumulator
-                              // (alpha/beta applied as integers, Cin int32)
+                              // (alpha/beta applied as integers, Cin int32);
+                              // alpha and beta then hold int32 bit patterns
+                              // (vkf_gemm_set_int_scalars), not floats
 #define VKF_GF_RS_SCALAR 128u // rs is one scalar (rs[0]) for every row
 #define VKF_GF_CS_SCALAR 256u // cs is one scalar (cs[0]) for every column
+#define VKF_GF_X_F16Q   512u  // int8 kernel: X holds fp16 values, quantised
+                              // on load to clamp(rint(x / xscale), -127, 127)
 
 #ifdef __cplusplus
+// Integer alpha / beta of a VKF_GF_D_I32 launch, stored bit for bit in the
+// float fields (every int32 value, including those above 2^24).
+inline void vkf_gemm_set_int_scalars(VkfGemmArgs &g, int32_t alpha, int32_t beta) {
+    __builtin_memcpy(&g.alpha, &alpha, 4);
+    __builtin_memcpy(&g.beta, &beta, 4);
+}
 static_assert(sizeof(VkfDequantArgs) == 24, "VkfDequantArgs layout");
 static_assert(sizeof(VkfQuantizeArgs) == 32, "VkfQuantizeArgs layout");
 static_assert(sizeof(VkfStreamArgs) == 24, "VkfStreamArgs layout");
 static_assert(sizeof(VkfQuantRowsArgs) == 48, "VkfQuantRowsArgs layout");
 static_assert(sizeof(VkfGemvArgs) == 64, "VkfGemvArgs layout");
-static_assert(sizeof(VkfGemmArgs) == 120, "VkfGemmArgs layout");
+static_assert(sizeof(VkfGemmArgs) == 176, "VkfGemmArgs layout");
 #endif

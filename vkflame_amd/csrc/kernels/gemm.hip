@@ -153,6 +153,72 @@ __device__ __forceinline__ Operand<ES, QT> make_operand(const void *P, uint64_t 
     return o;
 }
 
+// fp16 operand quantised to int8 while it is staged (the int8 linear of
+// kernels/linear_int8.glsl:63-70: q = clamp(round(x / act_scale), -127, 127),
+// here round-half-even, v_rndne, and an IEEE division).  Same tile geometry
+// as load_dense<1>: thread t covers rows t/8 + 32p, int8 elements
+// 16*(t%8) .. +15 of the 128-element step, i.e. 32 bytes of fp16 source.
+struct OperandF16Q {
+    const _Float16 *P;
+    uint64_t ld;  // elements
+    bool trans, fast;
+    uint32_t nrows, row0, K;
+    float s;
+    __device__ __forceinline__ static uint32_t q8(float x, float s) {
+        const float q = fminf(fmaxf(__builtin_rintf(x / s), -127.0f), 127.0f);
+        return (uint32_t)(int32_t)q & 0xffu;
+    }
+    __device__ __forceinline__ void load(uint32_t kt, TileRegs &t) const {
+        const uint32_t k = kt * 128 + 16 * (threadIdx.x & 7);
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t r = row0 + (threadIdx.x >> 3) + 32 * p;
+            uint32_t w[4] = {0, 0, 0, 0};
+            if (r < nrows) {
+                float x[16];
+                if (fast && k + 16 <= K) {
+                    const vkf_h8 h0 = *(const vkf_h8 *)(P + (uint64_t)r * ld + k);
+                    const vkf_h8 h1 = *(const vkf_h8 *)(P + (uint64_t)r * ld + k + 8);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        x[e] = (float)h0[e];
+                        x[8 + e] = (float)h1[e];
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const uint64_t idx = trans ? (uint64_t)(k + e) * ld + r : (uint64_t)r * ld + k + e;
+                        x[e] = k + e < K ? (float)P[idx] : 0.0f;
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 16; e++) w[e >> 2] |= q8(x[e], s) << (8 * (e & 3));
+            }
+            t.v[p] = vkf_i4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        }
+    }
+    __device__ __forceinline__ void store(uint8_t *lds, const TileRegs &t) const { store_dense(lds, t); }
+};
+
+// One 16x16 sub-tile product of a fragment pair, 16 bytes of K per lane on
+// both operands: one 16x16x32 fp16 MFMA, one 16x16x64 int8 MFMA, or for fp32
+// four 16x16x4 MFMAs, the e-th taking element e of each lane's four (K index
+// 4*(lane/16) + e of the 16-element slice, the same map on both operands).
+template <int ES, class ACC>
+__device__ __forceinline__ ACC mfma_frag(vkf_i4 a, vkf_i4 b, ACC c) {
+    if constexpr (ES == 2) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vkf_h8, a), __builtin_bit_cast(vkf_h8, b),
+                                                      c, 0, 0, 0);
+    } else if constexpr (ES == 1) {
+        return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+    } else {
+        const vkf_f4 fa = __builtin_bit_cast(vkf_f4, a), fb = __builtin_bit_cast(vkf_f4, b);
+#pragma unroll
+        for (int e = 0; e < 4; e++) c = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[e], fb[e], c, 0, 0, 0);
+        return c;
+    }
+}
+
 // One K step of the wave's 64x64 tile from LDS: two 16x16x32 fp16 MFMAs or
 // two 16x16x64 int8 MFMAs deep per 16x16 sub-tile.
 template <int ES, class ACC>
@@ -179,12 +245,7 @@ __device__ __forceinline__ void mfma_step(const uint8_t *lx, const uint8_t *ly, 
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                if constexpr (ES == 2)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vkf_h8, fa[s][i]),
-                                                                       __builtin_bit_cast(vkf_h8, fb[s][j]),
-                                                                       acc[i][j], 0, 0, 0);
-                else
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = mfma_frag<ES>(fa[s][i], fb[s][j], acc[i][j]);
             }
     __builtin_amdgcn_s_setprio(0);
 }
@@ -293,12 +354,7 @@ __device__ __forceinline__ void mfma_step_swz(const uint8_t *lx, const uint8_t *
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                if constexpr (ES == 2)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vkf_h8, fa[s][i]),
-                                                                       __builtin_bit_cast(vkf_h8, fb[s][j]),
-                                                                       acc[i][j], 0, 0, 0);
-                else
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = mfma_frag<ES>(fa[s][i], fb[s][j], acc[i][j]);
             }
     __builtin_amdgcn_s_setprio(0);
 }
@@ -991,6 +1047,25 @@ __device__ __forceinline__ void epilogue_tile(const VkfGemmArgs &a, uint32_t r0,
     epi_store<256>(a, r0, c0, (const float *)smem);
 }
 
+// The matrix of batch blockIdx.z of a dense launch (strided or through the
+// device pointer arrays).
+__device__ __forceinline__ VkfGemmArgs gemm_batch(const VkfGemmArgs &a0) {
+    VkfGemmArgs a = a0;
+    const uint32_t b = blockIdx.z;
+    if (a.bpx) {
+        a.X = a.bpx[b];
+        a.Y = a.bpy[b];
+        a.D = a.bpd[b];
+        a.Cin = a.D;
+    } else if (b) {
+        a.X = (const uint8_t *)a.X + b * a.bsx;
+        a.Y = (const uint8_t *)a.Y + b * a.bsy;
+        a.D = (uint8_t *)a.D + b * a.bsd;
+        if (a.Cin) a.Cin = (const uint8_t *)a.Cin + b * a.bsc;
+    }
+    return a;
+}
+
 // Workgroup -> 128 x 128 tile, XCD-aware.  Workgroups are dispatched to the
 // 8 XCDs round-robin (id % 8), each XCD with its own L2.  Columns (Y tiles)
 // are dealt to XCDs round-robin and an XCD runs all row tiles of a column
@@ -1055,7 +1130,7 @@ __device__ __forceinline__ void gemm_f16_body(const VkfGemmArgs &a) {
     epilogue_tile(a, r0, c0, acc, smem);
 }
 
-GEMM_KERNEL vkf_gemm_f16(VkfGemmArgs a) { gemm_f16_body<-1, -1>(a); }
+GEMM_KERNEL vkf_gemm_f16(VkfGemmArgs a0) { gemm_f16_body<-1, -1>(gemm_batch(a0)); }
 #define VKF_GEMM_Q(name, QT)                                                                        \
     GEMM_KERNEL vkf_gemm_##name##_f16(VkfGemmArgs a) { gemm_f16_body<-1, QT>(a); }
 #define VKF_GEMM_Q_Q81(name, QT)                                                                    \
@@ -1212,11 +1287,39 @@ VKF_GEMM_W(q5_k, VKF_Q5_K)
 VKF_GEMM_W(q6_k, VKF_Q6_K)
 
 // ---------------------------------------------------------------------------
+// fp32 x fp32 -> fp32 (hipblasSgemm and the fp32 hipblasGemmEx /
+// vkflame_dispatch_linear(FP32) the reference routes to its fp16 shader,
+// shim/hipblas_shim.cpp:84-113): v_mfma_f32_16x16x4_f32, 32 K per 128-byte
+// step, fp32 epilogue and fp32 D.
+// ---------------------------------------------------------------------------
+GEMM_KERNEL vkf_gemm_f32(VkfGemmArgs a0) {
+    const VkfGemmArgs a = gemm_batch(a0);
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_LDS_BOTH];
+    uint32_t r0, c0;
+    gemm_tile_of(r0, c0);
+    vkf_f4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
+    if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 4) &&
+        dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 4)) {
+        gemm_mainloop_dma<4>(a, r0, c0, acc, smem);
+    } else {
+        const auto ox = make_operand<4, -1>(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.R, r0, a.K);
+        const auto oy = make_operand<4, -1>(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.Cn, c0, a.K);
+        gemm_mainloop<4>(ox, oy, a.K, 32, acc, smem);
+    }
+    epilogue_tile(a, r0, c0, acc, smem);
+}
+
+// ---------------------------------------------------------------------------
 // int8 x int8 -> int32 (kernels/linear_int8.glsl:54-93, with int8 A).
 // flags & VKF_GF_D_F32 selects the float epilogue with fp32 D; VKF_GF_D_I32
 // stores the raw int32 accumulator.
 // ---------------------------------------------------------------------------
-GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a) {
+GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a0) {
+    const VkfGemmArgs a = gemm_batch(a0);
     __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_LDS_BOTH];
     uint32_t r0, c0;
     gemm_tile_of(r0, c0);
@@ -1225,8 +1328,20 @@ GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a) {
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = vkf_i4{0, 0, 0, 0};
-    if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 1) &&
-        dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 1)) {
+    if (a.flags & VKF_GF_X_F16Q) {  // fp16 activations quantised as they are staged
+        OperandF16Q ox;
+        ox.P = (const _Float16 *)a.X;
+        ox.ld = a.ldx;
+        ox.trans = (a.flags & VKF_GF_X_TRANS) != 0;
+        ox.fast = !ox.trans && (a.ldx % 8) == 0 && (((uintptr_t)a.X & 15) == 0);
+        ox.nrows = a.R;
+        ox.row0 = r0;
+        ox.K = a.K;
+        ox.s = a.xscale;
+        const auto oy = make_operand<1, -1>(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.Cn, c0, a.K);
+        gemm_mainloop<1>(ox, oy, a.K, 128, acc, smem);
+    } else if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 1) &&
+               dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 1)) {
         gemm_mainloop_dma<1>(a, r0, c0, acc, smem);
     } else {
         const auto ox = make_operand<1, -1>(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.R, r0, a.K);
@@ -1240,7 +1355,7 @@ GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a) {
     // raw int32 accumulator with integer alpha/beta (hipblasGemmEx, compute 32I)
     const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
     const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
-    const int32_t al = (int32_t)a.alpha, be = (int32_t)a.beta;
+    const int32_t al = __builtin_bit_cast(int32_t, a.alpha), be = __builtin_bit_cast(int32_t, a.beta);
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -1350,7 +1465,8 @@ __device__ __forceinline__ void epilogue_tile_k2(const VkfGemmArgs &a, uint32_t 
     epi_store<512>(a, r0, c0, (const float *)smem);
 }
 
-GEMM_KERNEL_K2 vkf_gemm_f16_k2(VkfGemmArgs a) {
+GEMM_KERNEL_K2 vkf_gemm_f16_k2(VkfGemmArgs a0) {
+    const VkfGemmArgs a = gemm_batch(a0);
     __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_K2_LDS];
     uint32_t r0, c0;
     gemm_tile_of(r0, c0);
@@ -1366,7 +1482,8 @@ GEMM_KERNEL_K2 vkf_gemm_f16_k2(VkfGemmArgs a) {
     epilogue_tile_k2(a, r0, c0, acc, smem, &pre);
 }
 
-GEMM_KERNEL_K2 vkf_gemm_i8_k2(VkfGemmArgs a) {
+GEMM_KERNEL_K2 vkf_gemm_i8_k2(VkfGemmArgs a0) {
+    const VkfGemmArgs a = gemm_batch(a0);
     __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_K2_LDS];
     uint32_t r0, c0;
     gemm_tile_of(r0, c0);
@@ -1387,7 +1504,7 @@ GEMM_KERNEL_K2 vkf_gemm_i8_k2(VkfGemmArgs a) {
     // raw int32 accumulator with integer alpha/beta (hipblasGemmEx, compute 32I)
     const int wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
     const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
-    const int32_t al = (int32_t)a.alpha, be = (int32_t)a.beta;
+    const int32_t al = __builtin_bit_cast(int32_t, a.alpha), be = __builtin_bit_cast(int32_t, a.beta);
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll

@@ -98,11 +98,15 @@ def stream_read(src: torch.Tensor, sink: torch.Tensor) -> None:
 
 
 def linear(A, B, M, N, K, dtype_code, transA=0, transB=1, act=0, C=None, alpha=None, beta=None, out=None):
-    """vkflame_dispatch_linear (row-major D[M,N] = act(alpha op(A) op(B) + beta C))."""
+    """vkflame_dispatch_linear (row-major D[M,N] = act(alpha op(A) op(B) + beta C)).
+    DTYPE_INT8 is the reference's int8 linear: fp16 A quantised by
+    act_scale = alpha, int8 B, C = per-channel w_scale (fp32 [N]), fp16 D.
+    DTYPE_INT8_INT32OUT: int8 A and B, exact int32 D, integer alpha / beta."""
     if out is None:
-        odt = {L.DTYPE_FP16: torch.float16, L.DTYPE_FP16_FP32OUT: torch.float32, L.DTYPE_INT8: torch.int32}[dtype_code]
+        odt = {L.DTYPE_FP16: torch.float16, L.DTYPE_FP16_FP32OUT: torch.float32, L.DTYPE_INT8: torch.float16,
+               L.DTYPE_INT8_INT32OUT: torch.int32, L.DTYPE_FP32: torch.float32}[dtype_code]
         out = torch.empty((M, N), dtype=odt, device=A.device)
-    if dtype_code == L.DTYPE_INT8:
+    if dtype_code == L.DTYPE_INT8_INT32OUT:
         al = ctypes.c_int32(1 if alpha is None else int(alpha))
         be = ctypes.c_int32(0 if beta is None else int(beta))
     else:

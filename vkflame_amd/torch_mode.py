@@ -136,7 +136,7 @@ def _int_mm(a, b):
     if M == 0 or N == 0 or K == 0:
         return NotImplemented
     with torch.cuda.device(a.device):
-        return ops.linear(oa[0], ob[0], M, N, K, L.DTYPE_INT8, transA=oa[1], transB=ob[1])
+        return ops.linear(oa[0], ob[0], M, N, K, L.DTYPE_INT8_INT32OUT, transA=oa[1], transB=ob[1])
 
 
 _HANDLERS = {
