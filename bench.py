@@ -146,7 +146,7 @@ def run_suite(torch, ops, O, replays, only=None):
     out = []
 
     def want(name):
-        return only is None or only in name
+        return only is None or any(o in name for o in only.split("|"))
 
     def gemv_line(name, qt, N, K, M, xkind, cfg, sub, quant=False):
         if not want(name):
@@ -343,7 +343,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-primary", action="store_true",
                     help="suite lines only, to stderr (profiling runs); no contract line")
-    ap.add_argument("--suite-only", default=None, help="run only suite lines whose name contains this")
+    ap.add_argument("--suite-only", default=None,
+                    help="run only suite lines whose name contains one of these '|'-separated strings")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run 10 plain device copies of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
