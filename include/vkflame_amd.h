@@ -107,6 +107,8 @@ int vkflame_quantize_rows_i8(const void *x, int x_dtype, int M, int K, int64_t l
  *    VKF_DTYPE_Q8_1 (Q8_1 blocks, row stride ldx bytes; 0 = packed).
  * M <= 16 runs the HBM-bound decode GEMV kernels, larger M the MFMA GEMM with
  * the weight tile dequantised into LDS.  K % block_elems == 0.
+ * With Q8_1 activations and M > 16, Q8_0 weights run on the int8 matrix
+ * cores: each 32-element block's dot is an exact int32, scaled by dx*dw in fp32.
  * With Q8_1 activations at M = 1, Q6_K weights use the exact integer dot
  * product (v_dot4_i32_i8), Q4_0, Q4_1, Q8_0, Q4_K and Q5_K the fp32 values
  * dx*q put on a 14-bit grid per 64 elements (as fp32 activations are); at
@@ -160,6 +162,12 @@ size_t vkflame_noalloc_scratch_bytes(void);
  * q8 * sc * (q6 - 32).  Exact int32; a test hook for the integer core of the
  * Q6_K x Q8_1 product. */
 int vkflame_q6_k_q8_1_partials(const void *w, const void *xq, int32_t *P, int M, int N, int K, void *stream);
+
+/* Integer partials of Q8_0 weights w[N, K] x Q8_1 activations xq[M, K] as the
+ * prefill's int8 matrix-core kernel computes them (the same MFMA code path):
+ * P[(m*N + n)*(K/32) + kb] = sum over block kb of q8x * q8w, exact int32.
+ * A test hook for the integer core of the Q8_0 x Q8_1 GEMM. */
+int vkflame_q8_0_q8_1_partials(const void *w, const void *xq, int32_t *P, int M, int N, int K, void *stream);
 
 /* Measurement hook: reads bytes (a multiple of 16) from src (16-byte
  * aligned) once with coalesced 16-byte loads and nothing else; sink is a

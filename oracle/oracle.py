@@ -136,6 +136,18 @@ def c_q6k_q8_1_partials(w: np.ndarray, xq: np.ndarray, M: int, N: int, K: int) -
     return P
 
 
+def np_q8_0_q8_1_partials(w: np.ndarray, xq: np.ndarray, M: int, N: int, K: int) -> np.ndarray:
+    """Exact integer block dots of Q8_0 weights [N, K] x Q8_1 activations
+    [M, K]: P[m, n, kb] = sum over block kb of q8x * q8w (the integer core of
+    ggml's vec_dot_q8_0_q8_1; codes at byte 2 of a Q8_0 block,
+    kernels/dequant_q8_0.glsl:23-27, and byte 4 of a Q8_1 block,
+    kernels/dequant_q8_1.glsl:26-31)."""
+    nb = K // 32
+    qw = np.ascontiguousarray(w, np.uint8).reshape(N, nb, 34)[:, :, 2:34].view(np.int8).astype(np.int64)
+    qx = np.ascontiguousarray(xq, np.uint8).reshape(M, nb, 36)[:, :, 4:36].view(np.int8).astype(np.int64)
+    return np.einsum("mbk,nbk->mnb", qx, qw).astype(np.int32)
+
+
 def c_act(act: int, x: float) -> float:
     return _C.lib().vkfo_act(act, x)
 

@@ -410,3 +410,41 @@ def test_config3_q4_k_prefill_5120x13824(dev):
     rows = np.concatenate([[0, N - 1], np.random.default_rng(6).choice(N, 512, replace=False)])
     wd = O.np_dequant(O.Q4_K, w[rows]).reshape(len(rows), K)
     assert rel_err(y[:, rows], O.ref_gemv(x.astype(np.float64), wd)) <= TOL_F32
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 300, 5120), (100, 203, 1056), (17, 130, 32)])
+def test_q8_0_q8_1_int8_partials_exact(dev, M, N, K):
+    """The integer core of the Q8_0 x Q8_1 prefill on the int8 matrix cores
+    (the GEMM's own MFMA code path): every block dot bit-exact against the
+    oracle, including K not a multiple of the 4-block step (K = 1056: rows of
+    33 blocks, so Q8_0 rows start 2 bytes off 4-byte alignment every other
+    row) and a single block."""
+    import torch
+    from vkflame_amd import ops
+    w = O.gen_weight(O.Q8_0, N, K, seed_for(3, 130) + K)
+    x = np.random.default_rng(seed_for(3, 131) + K).normal(0, 1, (M, K)).astype(np.float32)
+    xq = O.np_quantize_q8_1(x).reshape(M, -1)
+    P = ops.q8_0_q81_partials(to_dev(w, dev), to_dev(xq, dev), M, N, K)
+    torch.cuda.synchronize()
+    ref = O.np_q8_0_q8_1_partials(w, xq, M, N, K)
+    got = P.cpu().numpy()
+    assert np.array_equal(got, ref), int((got != ref).sum())
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 5120, 5120), (100, 203, 1056), (300, 1000, 4096)])
+def test_q8_0_q8_1_int8_prefill(dev, M, N, K):
+    """Q8_0 weights x Q8_1 activations at M > 16: exact block dots scaled by
+    dx*dw in fp32, against the float64 product of the dequantised operands
+    (which the exact dots reproduce up to the fp32 scaling and sum)."""
+    import torch
+    from vkflame_amd import ops
+    w = O.gen_weight(O.Q8_0, N, K, seed_for(3, 132) + K)
+    x = np.random.default_rng(seed_for(3, 133) + K).normal(0, 1, (M, K)).astype(np.float32)
+    xq = O.np_quantize_q8_1(x).reshape(M, -1)
+    y = ops.gemm_q(to_dev(w, dev), O.Q8_0, to_dev(xq, dev), N, K)
+    torch.cuda.synchronize()
+    rows = np.arange(N) if N <= 1000 else np.concatenate([[0, N - 1], np.random.default_rng(9).choice(N, 510, False)])
+    x64 = O.np_dequant(O.Q8_1, xq).reshape(M, K).astype(np.float64)
+    ref = O.ref_gemv(x64, O.np_dequant(O.Q8_0, w[rows]).reshape(len(rows), K))
+    err = rel_err(y.cpu().numpy()[:, rows], ref)
+    assert err <= 1e-5, err  # fp32 rounding of the scaled sums only

@@ -87,3 +87,29 @@ def test_ref_linear_int8_fp16a_exact_core():
     acc2, y2 = O.ref_linear_int8_fp16a(A * np.float16(0.5), W, 0.5, ws)
     assert np.array_equal(acc2, acc)  # (A/2) / 0.5 = A exactly
     assert np.allclose(y2, acc * ws[None, :] * 0.5, rtol=1e-6)
+
+
+def test_q8_0_q8_1_partials_known_answers_and_sums():
+    """Block dots of Q8_0 x Q8_1 codes: a hand-worked pair of blocks, and on
+    random blocks the sum over blocks equals the int8 GEMM of the codes
+    (vkfo_gemm_i8_nt) while each block equals its own slice's product."""
+    w = np.zeros((1, 34), np.uint8)
+    x = np.zeros((1, 36), np.uint8)
+    qw = np.arange(-16, 16, dtype=np.int8)
+    qx = np.full(32, 3, np.int8)
+    qx[0] = -127
+    w[0, 2:] = qw.view(np.uint8)
+    x[0, 4:] = qx.view(np.uint8)
+    # sum(3 * q) over q = -16..15 is -48, with q = -16 at index 0 weighted -127 instead of 3: -48 - 3*(-16) + (-127)*(-16)
+    assert O.np_q8_0_q8_1_partials(w, x, 1, 1, 32)[0, 0, 0] == -48 + 48 + 2032
+    M, N, K = 5, 7, 160
+    w = O.gen_weight(O.Q8_0, N, K, 21)
+    xq = O.np_quantize_q8_1(np.random.default_rng(22).normal(0, 1, (M, K)).astype(np.float32)).reshape(M, -1)
+    P = O.np_q8_0_q8_1_partials(w, xq, M, N, K)
+    codes_w = w.reshape(N, K // 32, 34)[:, :, 2:].reshape(N, K).view(np.int8)
+    codes_x = xq.reshape(M, K // 32, 36)[:, :, 4:].reshape(M, K).view(np.int8)
+    assert np.array_equal(P.astype(np.int64).sum(axis=2), O.c_gemm_i8_nt(codes_x, codes_w).astype(np.int64))
+    for kb in range(K // 32):
+        sl = slice(32 * kb, 32 * kb + 32)
+        assert np.array_equal(P[:, :, kb], O.c_gemm_i8_nt(np.ascontiguousarray(codes_x[:, sl]),
+                                                           np.ascontiguousarray(codes_w[:, sl])))

@@ -62,6 +62,7 @@ def lib() -> ctypes.CDLL:
     L.vkflame_noalloc_scratch_bytes.argtypes = []
     L.vkflame_noalloc_scratch_bytes.restype = ctypes.c_size_t
     L.vkflame_q6_k_q8_1_partials.argtypes = [P, P, P, I, I, I, P]
+    L.vkflame_q8_0_q8_1_partials.argtypes = [P, P, P, I, I, I, P]
     L.vkflame_stream_read.argtypes = [P, U64, P, P]
     L.vkflame_quantize_rows_i8.argtypes = [P, I, I, I, I64, P, P, P]
     L.vkflame_dispatch_linear.argtypes = [P, P, P, P, I, I, I, I, I, I, I, P, P, P]
@@ -72,7 +73,7 @@ def lib() -> ctypes.CDLL:
     L.vkflame_execute_launch.argtypes = [ctypes.POINTER(LaunchPlan), P]
     for f in ("vkflame_dispatch_dequant", "vkflame_quantize_q8_1", "vkflame_dispatch_gemm_q",
               "vkflame_dispatch_gemm_q_ws", "vkflame_dispatch_gemm_q_noalloc",
-              "vkflame_q6_k_q8_1_partials", "vkflame_dispatch_linear", "vkflame_dispatch_linear_int8",
+              "vkflame_q6_k_q8_1_partials", "vkflame_q8_0_q8_1_partials", "vkflame_dispatch_linear", "vkflame_dispatch_linear_int8",
               "vkflame_stream_read", "vkflame_quantize_rows_i8",
               "vkflame_resolve_launch", "vkflame_execute_launch", "vkflame_init",
               "vkflame_block_bytes", "vkflame_block_elems"):

@@ -325,6 +325,23 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
         return vkf::launch(gemv_kernel(qt, xk), dim3(cdiv(N, 4)), dim3(256), a, S(stream));
     }
     if (xk == 1) return kNotSup;  // prefill takes fp16 or Q8_1 activations
+    if (xk == 2 && qt == VKF_Q8_0) {
+        // Q8_1 x Q8_0: exact int32 block dots on the int8 matrix cores, each
+        // block's scales applied in fp32 (kernels/gemm.hip vkf_gemm_q8_0_q8_1_i8)
+        VkfGemmArgs g{};
+        g.X = x;
+        g.Y = w;
+        g.D = y;
+        g.ldx = (uint64_t)ldx;
+        g.ldy = row_bytes;
+        g.ldd = (uint64_t)ldy;
+        g.R = (uint32_t)M;
+        g.Cn = (uint32_t)N;
+        g.K = (uint32_t)K;
+        g.alpha = 1.0f;
+        g.flags = VKF_GF_D_F32;
+        return vkf::launch(VKF_K_GEMM_Q8_0_Q81_I8, dim3(cdiv(N, 128), cdiv(M, 128)), dim3(512), g, S(stream));
+    }
     if (xk == 2 && workspace && workspace_bytes >= vkflame_gemm_q_workspace_bytes(x_dtype, M, K) &&
         aligned(workspace, 16) && ldx == (int64_t)(K / 32) * 36) {
         // decode the activations once (fp16(d*q), the value the Q8_1 GEMM's
@@ -390,6 +407,22 @@ int vkflame_q6_k_q8_1_partials(const void *w, const void *xq, int32_t *P, int M,
         if (e != kOk) return e;
     }
     return kOk;
+}
+
+int vkflame_q8_0_q8_1_partials(const void *w, const void *xq, int32_t *P, int M, int N, int K, void *stream) {
+    if (M < 0 || N < 0 || K < 0 || (K % 32) != 0) return kInval;
+    if (M == 0 || N == 0 || K == 0) return kOk;
+    if (!w || !xq || !P || !aligned(w, 2) || !aligned(xq, 4) || !aligned(P, 4)) return kInval;
+    VkfGemmArgs g{};
+    g.X = xq;
+    g.Y = w;
+    g.D = P;
+    g.ldx = (uint64_t)(K / 32) * 36;
+    g.ldy = (uint64_t)(K / 32) * 34;
+    g.R = (uint32_t)M;
+    g.Cn = (uint32_t)N;
+    g.K = (uint32_t)K;
+    return vkf::launch(VKF_K_Q8_0_Q8_1_PARTIALS, dim3(cdiv(N, 128), cdiv(M, 128)), dim3(512), g, S(stream));
 }
 
 int vkflame_dispatch_linear(const void *A, const void *B, const void *C, void *D, int M, int N, int K, int dtype,

@@ -147,7 +147,9 @@
     X(GEMM_K2_Q5_0_F16, "vkf_gemm_q5_0_f16_k2")             \
     X(GEMM_K2_Q4_K_F16, "vkf_gemm_q4_k_f16_k2")             \
     X(GEMM_K2_Q5_K_F16, "vkf_gemm_q5_k_f16_k2")             \
-    X(GEMM_K2_Q6_K_F16, "vkf_gemm_q6_k_f16_k2")
+    X(GEMM_K2_Q6_K_F16, "vkf_gemm_q6_k_f16_k2")             \
+    X(GEMM_Q8_0_Q81_I8, "vkf_gemm_q8_0_q8_1_i8")            \
+    X(Q8_0_Q8_1_PARTIALS, "vkf_q8_0_q8_1_partials_mfma")
 
 enum VkfKernelId {
 #define VKF_X(id, sym) VKF_K_##id,

@@ -971,20 +971,21 @@ __device__ __forceinline__ EpiPre epi_prefetch(const VkfGemmArgs &a, uint32_t r0
     return p;
 }
 
-template <class ACC>
-__device__ __forceinline__ void epi_stage(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC acc[4][4],
-                                          float *tile, int wr, int wc, const EpiPre *pre = nullptr) {
+// NI < 4: the wave holds only 16-row groups i0 .. i0 + NI - 1 of its 64 rows.
+template <int NI = 4, class ACC>
+__device__ __forceinline__ void epi_stage(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC acc[][4],
+                                          float *tile, int wr, int wc, const EpiPre *pre = nullptr, int i0 = 0) {
     constexpr int TP = 132;
     const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
     const EpiPre p = pre ? *pre : epi_prefetch(a, r0, c0, wr, wc);
     const float *csv = p.cs, *bcv = p.bc;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < NI; i++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int tr = wr * 64 + 16 * i + 4 * lg + e;
+            const int tr = wr * 64 + 16 * (i0 + i) + 4 * lg + e;
             const uint32_t r = r0 + tr, rr = r < a.R ? r : a.R - 1;
-            const float rsv = p.rs[4 * i + e];
+            const float rsv = p.rs[4 * (i0 + i) + e];
             float brv = 0.0f;
             if (a.bias && (a.flags & VKF_GF_BIAS_ROW))
                 brv = (a.flags & VKF_GF_BIAS_F32) ? ((const float *)a.bias)[rr] : (float)((const _Float16 *)a.bias)[rr];
@@ -1285,6 +1286,161 @@ VKF_GEMM_W(q5_0, VKF_Q5_0)
 VKF_GEMM_W(q4_k, VKF_Q4_K)
 VKF_GEMM_W(q5_k, VKF_Q5_K)
 VKF_GEMM_W(q6_k, VKF_Q6_K)
+
+// ---------------------------------------------------------------------------
+// Q8_1 activations x Q8_0 weights on the int8 matrix cores
+// (vkf_gemm_q8_0_q8_1_i8): ggml's block dot, y[m, n] = sum over 32-element
+// blocks kb of dx[m,kb] * dw[n,kb] * P[m,n,kb], with P = sum q8x * q8w the
+// exact int32 dot of the block's codes (kernels/dequant_q8_1.glsl:21-32,
+// kernels/dequant_q8_0.glsl:18-28; shim/hip_runtime_shim.cpp:1151-1166 is the
+// reference's quantised mul_mat that dequantises both to fp32 instead).
+// One v_mfma_i32_16x16x32_i8 per 16x16 sub-tile and block yields P exactly
+// (|P| <= 32 * 128 * 128 = 2^19); the block's scales are applied to it in
+// fp32: acc += float(P) * (dx * dw).  The fold is three VALU operations per
+// output and block (convert, scale product, fma), three times the MFMA time
+// of the block, so the kernel is built to keep the VALU busy: a 128 x 128
+// tile per 512-thread workgroup, eight waves of 32 x 64 (two per SIMD, so
+// that one wave's fold issues while the other waits on its MFMAs and LDS
+// reads).  Wave w covers columns 64 * (w & 1) and rows 64 * ((w >> 1) & 1)
+// + 32 * (w >> 2) of the tile.  K advances 4 blocks per step: thread t loads
+// block t & 3 of activation row t >> 2 and of weight row t >> 2 into
+// registers before the step's MFMAs and writes its codes (XOR-swizzled as
+// in the direct-to-LDS tiles) and scales to the other LDS stage after them.
+// PARTIALS: store every P (int32) at D[(m*N + n)*(K/32) + kb] instead (the
+// integer core, for tests).
+// ---------------------------------------------------------------------------
+#define QI_STAGE (2 * 16384 + 2 * 2048)  // X codes, Y codes, dx[4][128], dw[4][128]
+#define QI_LDS (2 * QI_STAGE > 128 * 132 * 4 ? 2 * QI_STAGE : 128 * 132 * 4)
+
+struct Q8Stage {
+    uint32_t x[9], w[9], wsh;
+    bool xv, wv;
+};
+
+__device__ __forceinline__ void q8_stage_load(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, uint32_t kt,
+                                              Q8Stage &s) {
+    const uint32_t tr = threadIdx.x >> 2, nb = a.K / 32, kb = 4 * kt + (threadIdx.x & 3);
+    const uint32_t rx = r0 + tr < a.R ? r0 + tr : a.R - 1, ry = c0 + tr < a.Cn ? c0 + tr : a.Cn - 1;
+    const uint32_t kk = kb < nb ? kb : nb - 1;
+    s.xv = kb < nb && r0 + tr < a.R;
+    s.wv = kb < nb && c0 + tr < a.Cn;
+    // Q8_1: 36-byte blocks, 4-byte aligned: fp16 d, fp16 s, int8 q[32]
+    const uint8_t *px = (const uint8_t *)a.X + (uint64_t)rx * a.ldx + 36ull * kk;
+    const vkf_u4 x0 = *(const vkf_u4a4 *)px, x1 = *(const vkf_u4a4 *)(px + 16);
+    s.x[0] = x0[0]; s.x[1] = x0[1]; s.x[2] = x0[2]; s.x[3] = x0[3];
+    s.x[4] = x1[0]; s.x[5] = x1[1]; s.x[6] = x1[2]; s.x[7] = x1[3];
+    s.x[8] = *(const uint32_t *)(px + 32);
+    // Q8_0: 34-byte blocks, 2-byte aligned: the covering dwords, realigned
+    // when stored; nothing past the block's last byte is read
+    const uint8_t *pw = (const uint8_t *)a.Y + (uint64_t)ry * a.ldy + 34ull * kk;
+    const uint32_t sh = (uint32_t)(uintptr_t)pw & 3u;
+    const uint8_t *aw = pw - sh;
+    const vkf_u4 w0 = *(const vkf_u4a4 *)aw, w1 = *(const vkf_u4a4 *)(aw + 16);
+    s.w[0] = w0[0]; s.w[1] = w0[1]; s.w[2] = w0[2]; s.w[3] = w0[3];
+    s.w[4] = w1[0]; s.w[5] = w1[1]; s.w[6] = w1[2]; s.w[7] = w1[3];
+    s.w[8] = sh ? *(const uint32_t *)(aw + 32) : (uint32_t)*(const uint16_t *)(pw + 32);
+    s.wsh = sh;
+}
+
+__device__ __forceinline__ void q8_stage_store(uint8_t *stage, const Q8Stage &s) {
+    const uint32_t tr = threadIdx.x >> 2, bi = threadIdx.x & 3;
+    uint8_t *cx = stage + tr * 128, *cw = stage + 16384 + tr * 128;
+    float *dx = (float *)(stage + 32768), *dw = (float *)(stage + 32768 + 2048);
+    const uint32_t *xq = &s.x[1];
+    uint32_t wq[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) wq[i] = s.wsh ? s.w[i + 1] : realign(s.w[i], s.w[i + 1], 2);
+    const uint32_t dwb = realign(s.w[0], s.w[1], s.wsh) & 0xffffu;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t off = ((2 * bi + h) ^ (tr & 7)) << 4;
+        *(vkf_u4 *)(cx + off) = s.xv ? vkf_u4{xq[4 * h], xq[4 * h + 1], xq[4 * h + 2], xq[4 * h + 3]}
+                                     : vkf_u4{0, 0, 0, 0};
+        *(vkf_u4 *)(cw + off) = s.wv ? vkf_u4{wq[4 * h], wq[4 * h + 1], wq[4 * h + 2], wq[4 * h + 3]}
+                                     : vkf_u4{0, 0, 0, 0};
+    }
+    dx[bi * 128 + tr] = s.xv ? vkf_h2f((uint16_t)(s.x[0] & 0xffffu)) : 0.0f;
+    dw[bi * 128 + tr] = s.wv ? vkf_h2f((uint16_t)dwb) : 0.0f;
+}
+
+template <bool PARTIALS>
+__device__ __forceinline__ void gemm_q8_i8_body(const VkfGemmArgs &a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[QI_LDS];
+    uint32_t r0, c0;
+    gemm_tile_of(r0, c0);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wc = wave & 1, wr = (wave >> 1) & 1, i0 = 2 * (wave >> 2);
+    const int li = lane & 15, lg = lane >> 4;
+    const uint32_t nb = a.K / 32, nk = (nb + 3) / 4;
+    vkf_f4 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
+    Q8Stage st;
+    q8_stage_load(a, r0, c0, 0, st);
+    q8_stage_store(smem, st);
+    __syncthreads();
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        if (kt + 1 < nk) q8_stage_load(a, r0, c0, kt + 1, st);
+        const uint8_t *stage = smem + (kt & 1) * QI_STAGE;
+        const float *dx = (const float *)(stage + 32768), *dw = (const float *)(stage + 32768 + 2048);
+#pragma unroll 1
+        for (int b = 0; b < 4; b++) {
+            // 8 bytes of the block per lane: k-slice 8*lg, inside chunk 2b + lg/2
+            const uint32_t c = 2 * b + (lg >> 1), off = 8 * (lg & 1);
+            long fb[4];
+            float sw[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t cc = wc * 64 + 16 * j + li;
+                fb[j] = *(const long *)(stage + 16384 + cc * 128 + ((c ^ (cc & 7)) << 4) + off);
+                sw[j] = dw[b * 128 + cc];
+            }
+            // the block's 8 dots first (independent results, so the MFMAs
+            // issue back to back), then their folds
+            vkf_i4 P[2][4];
+            vkf_f4 sx[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const uint32_t rr = wr * 64 + 16 * (i0 + i) + li;
+                const long fa = *(const long *)(stage + rr * 128 + ((c ^ (rr & 7)) << 4) + off);
+                sx[i] = *(const vkf_f4 *)(dx + b * 128 + wr * 64 + 16 * (i0 + i) + 4 * lg);
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    P[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa, fb[j], vkf_i4{0, 0, 0, 0}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    if constexpr (PARTIALS) {
+                        const uint32_t kb = 4 * kt + b, n = c0 + wc * 64 + 16 * j + li;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const uint32_t m = r0 + wr * 64 + 16 * (i0 + i) + 4 * lg + e;
+                            if (m < a.R && n < a.Cn && kb < nb)
+                                ((int32_t *)a.D)[((uint64_t)m * a.Cn + n) * nb + kb] = P[i][j][e];
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            acc[i][j][e] = fmaf((float)P[i][j][e], sx[i][e] * sw[j], acc[i][j][e]);
+                    }
+                }
+        }
+        if (kt + 1 < nk) q8_stage_store(smem + ((kt + 1) & 1) * QI_STAGE, st);
+        __syncthreads();
+    }
+    if constexpr (!PARTIALS) {
+        epi_stage<2>(a, r0, c0, acc, (float *)smem, wr, wc, nullptr, i0);
+        __syncthreads();
+        epi_store<512>(a, r0, c0, (const float *)smem);
+    }
+}
+
+GEMM_KERNEL_W vkf_gemm_q8_0_q8_1_i8(VkfGemmArgs a) { gemm_q8_i8_body<false>(a); }
+GEMM_KERNEL_W vkf_q8_0_q8_1_partials_mfma(VkfGemmArgs a) { gemm_q8_i8_body<true>(a); }
 
 // ---------------------------------------------------------------------------
 // fp32 x fp32 -> fp32 (hipblasSgemm and the fp32 hipblasGemmEx /

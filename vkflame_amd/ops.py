@@ -78,6 +78,13 @@ def q6k_q81_partials(w: torch.Tensor, xq: torch.Tensor, M: int, N: int, K: int) 
     return P
 
 
+def q8_0_q81_partials(w: torch.Tensor, xq: torch.Tensor, M: int, N: int, K: int) -> torch.Tensor:
+    """Exact int32 block dots of Q8_0 weights x Q8_1 activations, [M, N, K/32]."""
+    P = torch.empty((M, N, K // 32), dtype=torch.int32, device=w.device)
+    check(lib().vkflame_q8_0_q8_1_partials(_p(w), _p(xq), _p(P), M, N, K, _stream()), "q8_0_q81_partials")
+    return P
+
+
 def quantize_rows_i8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """fp16 / fp32 [M, K] -> (int8 [M, K], fp32 scale [M]): symmetric per-row
     quantisation (vkflame_quantize_rows_i8)."""
