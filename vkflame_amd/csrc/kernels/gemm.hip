@@ -1197,34 +1197,49 @@ __device__ __forceinline__ void gemm_mainloop_wide(const VkfGemmArgs &a, uint32_
     };
     if constexpr (has_qhalf<QT>()) {
         // all eight waves decode: thread t -> row t/4, elements 16(t&3) ..
+        // Weight chunks are loaded two steps ahead of their MFMA step, into
+        // two alternating register sets, so that a chunk's HBM latency hides
+        // under two MFMA steps; activation tiles (mostly L2 hits) one step
+        // ahead.  Step kt issues activation tile kt+1, then weight chunk
+        // kt+2, so the compiler's s_waitcnt before the decode of chunk kt+1
+        // (which lets only chunk kt+2's loads stay in flight; loads return
+        // in order) also covers activation tile kt+1 before the barrier.
         const uint32_t hr = threadIdx.x >> 2, hq = threadIdx.x & 3;
         auto store_h = [&](uint32_t stage, const vkf_i4 v[2]) {
             uint8_t *sy = smem + stage * GEMM_W_STAGE + 32768 + hr * 128;
 #pragma unroll
             for (int g = 0; g < 2; g++) *(vkf_i4 *)(sy + (((2 * hq + g) ^ (hr & 7)) << 4)) = v[g];
         };
-        QHalf<QT> q;
+        const uint8_t *W = (const uint8_t *)a.Y;
+        QHalf<QT> qa, qb;
         vkf_i4 tv[2];
         issue_x(0, 0);
-        q.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, 0);
-        q.decode(tv);
+        qa.load(W, a.ldy, a.Cn, c0, a.K, 0);
+        qb.load(W, a.ldy, a.Cn, c0, a.K, 64);
+        qa.decode(tv);
         store_h(0, tv);
         wait_vm<0>();
         __syncthreads();
-        for (uint32_t kt = 0; kt < nk; kt++) {
+        // qn holds chunk kt+1 (loaded a step earlier), qf is free.  The
+        // weight loads and decodes are unconditional (chunks past the end
+        // are clamped in-bounds loads decoded to zeros into a stage that is
+        // not read again), so that the compiler's wait analysis sees the
+        // same loads in flight on every path and never falls back to
+        // vmcnt(0) at a merge point.  K is whole 256-element super-blocks,
+        // so nk is a multiple of 4 and the loop runs its steps in pairs.
+        auto step = [&](uint32_t kt, QHalf<QT> &qn, QHalf<QT> &qf) {
             const uint32_t cur = kt & 1;
-            if (kt + 1 < nk) {
-                issue_x(kt + 1, cur ^ 1);
-                q.load((const uint8_t *)a.Y, a.ldy, a.Cn, c0, a.K, (kt + 1) * 64);
-            }
+            if (kt + 1 < nk) issue_x(kt + 1, cur ^ 1);
+            qf.load(W, a.ldy, a.Cn, c0, a.K, (kt + 2) * 64);
             const uint8_t *lx = smem + cur * GEMM_W_STAGE;
             mfma_step_swz<2>(lx, lx + 32768, wr, wc, acc);
-            if (kt + 1 < nk) {
-                q.decode(tv);
-                store_h(cur ^ 1, tv);
-            }
-            wait_vm<0>();
+            qn.decode(tv);
+            store_h(cur ^ 1, tv);
             __syncthreads();
+        };
+        for (uint32_t kt = 0; kt < nk; kt += 2) {
+            step(kt, qb, qa);
+            step(kt + 1, qa, qb);
         }
         return;
     }
