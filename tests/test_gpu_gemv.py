@@ -108,6 +108,20 @@ def test_q6_k_q8_1_partials_bit_exact(dev):
     assert bits_equal(P.cpu().numpy(), ref), first_mismatch(P.cpu().numpy(), ref)
 
 
+def test_q6_k_q8_1_partials_config5_k(dev):
+    """At C5's K = 5120: 20 super-blocks and 160 Q8_1 blocks per row, 48
+    generated weight rows against 4 activation rows."""
+    import torch
+    from vkflame_amd import ops
+    N, K, M = 48, 5120, 4
+    w = O.gen_weight(O.Q6_K, N, K, seed_for(5, 8))
+    xq, _ = _x("q8_1", M, K, seed_for(5, 9))
+    P = ops.q6k_q81_partials(to_dev(w, dev), to_dev(xq, dev), M, N, K)
+    torch.cuda.synchronize()
+    ref = O.c_q6k_q8_1_partials(w, xq, M, N, K)
+    assert bits_equal(P.cpu().numpy(), ref), first_mismatch(P.cpu().numpy(), ref)
+
+
 def test_q6_k_q8_1_partials_extreme_scales(dev):
     """Scales across the whole int8 range (|sc*(q-32)| up to 4096)."""
     import torch
