@@ -86,7 +86,10 @@ def time_graph(torch, launches, replays: int, warmup_launches: int = 0) -> list[
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    # captured on the warm-up stream: launches that keep per-stream state
+    # (the stream-K GEMM's workspace, made on a stream's first eager call)
+    # find it there
+    with torch.cuda.graph(g, stream=s):
         for f in launches:
             f()
     for _ in range(max(1, math.ceil(warmup_launches / len(launches)))):
