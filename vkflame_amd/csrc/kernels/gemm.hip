@@ -85,10 +85,92 @@ __device__ __forceinline__ void load_dense(const void *P, uint64_t ld, bool tran
     }
 }
 
+// Transposed dense operand (stored [K, rows]: element (r, k) at P + (k*ld +
+// r)*ES, e.g. B [K, N] of an NN product): thread t covers rows 4*(t/8) + i
+// (i < 4) of the tile and the 16-byte K piece t%8 of the step.  Its EPC
+// values of k are loaded along the contiguous row direction (the 4 rows'
+// elements of one k in one 4*ES-byte load) and transposed in registers into
+// the same 16-byte row pieces the K-contiguous loads produce: fp16 one
+// v_perm per output dword, int8 three, fp32 none.  vec: the row pitch and
+// base allow those loads; groups of 4 rows that cross the last row, and
+// unaligned operands, load element by element.
+template <int ES>
+__device__ __forceinline__ void load_dense_t(const void *P, uint64_t ld, bool vec, uint32_t nrows, uint32_t row0,
+                                             uint32_t K, uint32_t k0, TileRegs &t) {
+    constexpr int EPC = 16 / ES;
+    const uint32_t kb = k0 + EPC * (threadIdx.x & 7), r = row0 + 4 * (threadIdx.x >> 3);
+    const uint8_t *B = (const uint8_t *)P;
+    if (vec && r + 4 <= nrows) {
+        if constexpr (ES == 2) {
+            uint32_t in[8][2];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                if (kb + e < K) {
+                    const uint2 v = *(const uint2 *)(B + ((uint64_t)(kb + e) * ld + r) * 2);
+                    in[e][0] = v.x;
+                    in[e][1] = v.y;
+                } else {
+                    in[e][0] = in[e][1] = 0;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int d = 0; d < 4; d++)  // (row i, k 2d) low, (row i, k 2d+1) high
+                    t.v[i][d] = (int)__builtin_amdgcn_perm(in[2 * d + 1][i >> 1], in[2 * d][i >> 1],
+                                                           (i & 1) ? 0x07060302u : 0x05040100u);
+        } else if constexpr (ES == 1) {
+            uint32_t in[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) in[e] = kb + e < K ? *(const uint32_t *)(B + (uint64_t)(kb + e) * ld + r) : 0u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                // bytes (row i of in[lo], row i of in[lo + 1]) in the low half
+                const uint32_t sel = (uint32_t)i | ((uint32_t)(4 + i) << 8) | 0x0c0c0000u;
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const uint32_t a = __builtin_amdgcn_perm(in[4 * d + 1], in[4 * d], sel);
+                    const uint32_t b = __builtin_amdgcn_perm(in[4 * d + 3], in[4 * d + 2], sel);
+                    t.v[i][d] = (int)__builtin_amdgcn_perm(b, a, 0x05040100u);
+                }
+            }
+        } else {
+            vkf_i4 in[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                in[e] = kb + e < K ? *(const vkf_i4 *)(B + ((uint64_t)(kb + e) * ld + r) * 4) : vkf_i4{0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 4; i++) t.v[i] = vkf_i4{in[0][i], in[1][i], in[2][i], in[3][i]};
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint8_t bytes[16];
+#pragma unroll
+        for (int e = 0; e < EPC; e++) {
+            const bool in = r + i < nrows && kb + e < K;
+            const uint64_t idx = (uint64_t)(kb + e) * ld + r + i;
+#pragma unroll
+            for (int q = 0; q < ES; q++) bytes[e * ES + q] = in ? B[idx * ES + q] : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            t.v[i][j] = (int)((uint32_t)bytes[4 * j] | ((uint32_t)bytes[4 * j + 1] << 8) |
+                              ((uint32_t)bytes[4 * j + 2] << 16) | ((uint32_t)bytes[4 * j + 3] << 24));
+    }
+}
+
 __device__ __forceinline__ void store_dense(uint8_t *lds, const TileRegs &t) {
 #pragma unroll
     for (int p = 0; p < 4; p++)
         *(vkf_i4 *)(lds + ((threadIdx.x >> 3) + 32 * p) * GP + 16 * (threadIdx.x & 7)) = t.v[p];
+}
+
+// The pieces of load_dense_t: rows 4*(t/8) + p.
+__device__ __forceinline__ void store_dense_t(uint8_t *lds, const TileRegs &t) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) *(vkf_i4 *)(lds + (4 * (threadIdx.x >> 3) + p) * GP + 16 * (threadIdx.x & 7)) = t.v[p];
 }
 
 // Quantised operand tile dequantised to fp16: 128 rows x 64 k.  Thread t
@@ -127,14 +209,16 @@ template <int ES, int QT>
 struct Operand {
     const void *P;
     uint64_t ld;  // elements (dense) or bytes per row (quantised)
-    bool trans, fast;
+    bool trans, fast;  // fast: K-contiguous 16-byte pieces; for trans, load_dense_t's vector loads
     uint32_t nrows, row0, K;
     __device__ __forceinline__ void load(uint32_t kt, TileRegs &t) const {
         if constexpr (QT >= 0) load_quant<QT>((const uint8_t *)P, ld, nrows, row0, K, kt * (GK / 2), t);
-        else load_dense<ES>(P, ld, trans, fast, nrows, row0, K, kt * (GK / ES), t);
+        else if (trans) load_dense_t<ES>(P, ld, fast, nrows, row0, K, kt * (GK / ES), t);
+        else load_dense<ES>(P, ld, false, fast, nrows, row0, K, kt * (GK / ES), t);
     }
     __device__ __forceinline__ void store(uint8_t *lds, const TileRegs &t) const {
         if constexpr (QT >= 0) store_quant(lds, t);
+        else if (trans) store_dense_t(lds, t);
         else store_dense(lds, t);
     }
 };
@@ -146,7 +230,8 @@ __device__ __forceinline__ Operand<ES, QT> make_operand(const void *P, uint64_t 
     o.P = P;
     o.ld = ld;
     o.trans = trans;
-    o.fast = !trans && ((ld * ES) % 16) == 0 && (((uintptr_t)P & 15) == 0);
+    o.fast = trans ? ((ld * ES) % (4 * ES)) == 0 && (((uintptr_t)P % (4 * ES)) == 0)
+                   : ((ld * ES) % 16) == 0 && (((uintptr_t)P & 15) == 0);
     o.nrows = nrows;
     o.row0 = row0;
     o.K = K;
@@ -936,6 +1021,60 @@ __device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_
     }
 }
 
+// Dense X K-contiguous (direct-to-LDS tiles) and Y transposed (stored
+// [K, C], e.g. B [K, N] of an NN product, torch.mm(a, b) with contiguous b):
+// Y's 16-byte row pieces come from load_dense_t (loads along Y's contiguous
+// direction, transposed in registers), loaded a step ahead and stored into
+// the swizzled LDS layout after the step's MFMAs, as the quantised weight
+// tiles of gemm_mainloop_qdma.  K*ES a multiple of 128 (X's condition).
+template <int ES, class ACC>
+__device__ __forceinline__ void gemm_mainloop_tdma(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, ACC acc[4][4],
+                                                   uint8_t *smem) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wr = wave >> 1, wc = wave & 1;
+    const uint32_t nk = (uint32_t)(((uint64_t)a.K * ES) / 128);
+    const uint8_t *gx[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t rr = (4 * wave + j) * 8 + (lane >> 3);
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t rx = r0 + rr < a.R ? r0 + rr : a.R - 1;
+        gx[j] = (const uint8_t *)a.X + (uint64_t)rx * a.ldx * ES + ch * 16;
+    }
+    auto issue_x = [&](uint32_t kt, uint32_t stage) {
+        uint8_t *sx = smem + stage * 32768;
+#pragma unroll
+        for (int j = 0; j < 4; j++) vkf_load_lds16(gx[j] + (uint64_t)kt * 128, sx + (4 * wave + j) * 1024);
+    };
+    const auto oy = make_operand<ES, -1>(a.Y, a.ldy, true, a.Cn, c0, a.K);
+    const uint32_t yr = 4 * (threadIdx.x >> 3), yc = threadIdx.x & 7;
+    auto store_y = [&](uint32_t stage, const TileRegs &t) {
+        uint8_t *sy = smem + stage * 32768 + 16384;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t r = yr + p;
+            *(vkf_i4 *)(sy + r * 128 + ((yc ^ (r & 7)) << 4)) = t.v[p];
+        }
+    };
+    TileRegs ty;
+    issue_x(0, 0);
+    oy.load(0, ty);
+    store_y(0, ty);
+    wait_vm<0>();
+    __syncthreads();
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        const uint32_t cur = kt & 1;
+        if (kt + 1 < nk) {
+            issue_x(kt + 1, cur ^ 1);
+            oy.load(kt + 1, ty);
+        }
+        const uint8_t *lx = smem + cur * 32768;
+        mfma_step_swz<ES>(lx, lx + 16384, wr, wc, acc);
+        if (kt + 1 < nk) store_y(cur ^ 1, ty);
+        wait_vm<0>();
+        __syncthreads();
+    }
+}
+
 // Float epilogue of the workgroup's 128x128 tile (v = alpha * acc * rs[r] *
 // cs[c] + beta * Cin + bias, then the activation):
 // each lane finishes its 64 values, the tile is staged as fp32 rows in LDS
@@ -1106,12 +1245,14 @@ __device__ __forceinline__ void gemm_f16_body(const VkfGemmArgs &a) {
     // kernels with dense fp16 X hold either main loop's buffers
     __shared__ __attribute__((aligned(16))) uint8_t smem[XQT < 0 ? GEMM_LDS_BOTH : GEMM_LDS];
     if constexpr (XQT < 0 && QT < 0) {
-        if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 2) &&
-            dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 2)) {
-            gemm_mainloop_dma<2>(a, r0, c0, acc, smem);
+        if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 2)) {
+            if (dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 2)) gemm_mainloop_dma<2>(a, r0, c0, acc, smem);
+            else if (a.flags & VKF_GF_Y_TRANS) gemm_mainloop_tdma<2>(a, r0, c0, acc, smem);
+            else goto general;
             epilogue_tile(a, r0, c0, acc, smem);
             return;
         }
+    general:;
     }
     if constexpr (XQT < 0 && QT >= 0) {
         if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 2)) {
@@ -1476,6 +1617,8 @@ GEMM_KERNEL vkf_gemm_f32(VkfGemmArgs a0) {
     if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 4) &&
         dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 4)) {
         gemm_mainloop_dma<4>(a, r0, c0, acc, smem);
+    } else if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 4) && (a.flags & VKF_GF_Y_TRANS)) {
+        gemm_mainloop_tdma<4>(a, r0, c0, acc, smem);
     } else {
         const auto ox = make_operand<4, -1>(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.R, r0, a.K);
         const auto oy = make_operand<4, -1>(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.Cn, c0, a.K);
@@ -1514,6 +1657,8 @@ GEMM_KERNEL vkf_gemm_i8(VkfGemmArgs a0) {
     } else if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 1) &&
                dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 1)) {
         gemm_mainloop_dma<1>(a, r0, c0, acc, smem);
+    } else if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 1) && (a.flags & VKF_GF_Y_TRANS)) {
+        gemm_mainloop_tdma<1>(a, r0, c0, acc, smem);
     } else {
         const auto ox = make_operand<1, -1>(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.R, r0, a.K);
         const auto oy = make_operand<1, -1>(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.Cn, c0, a.K);
