@@ -542,7 +542,7 @@ __device__ __forceinline__ void gemv_dot_lds(const VkfGemvArgs &a, unsigned char
             const uint32_t nn = tile * TR + rr < a.N ? tile * TR + rr : a.N - 1;
             const uint32_t off = r0 + 16 * (pp - rr * PR);
             if (64 * j + 63 < NP || P < NP)  // lanes past the region's pieces issue nothing (fewer L1 accesses)
-                vkf_load_lds16(a.w + (uint64_t)nn * a.row_bytes + (off < last ? off : last), buf + 64 * j * 16);
+                vkf_load_lds16_nt(a.w + (uint64_t)nn * a.row_bytes + (off < last ? off : last), buf + 64 * j * 16);
         }
         __builtin_amdgcn_s_setprio(0);
         if (it == iters - 1 && straddle) {

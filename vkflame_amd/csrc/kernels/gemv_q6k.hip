@@ -246,7 +246,7 @@ __device__ __forceinline__ void gemv_q6k_q81(const VkfGemvArgs &a, unsigned char
                 const uint32_t P = 64 * j + lane, pp = P < NP ? P : NP - 1, rr = pp / PR;
                 const uint32_t nn = tile * TR + rr < a.N ? tile * TR + rr : a.N - 1;
                 const uint32_t off = r0 + 16 * (pp - rr * PR);
-                vkf_load_lds16(a.w + (uint64_t)nn * a.row_bytes + (off < last ? off : last), buf + 64 * j * 16);
+                vkf_load_lds16_nt(a.w + (uint64_t)nn * a.row_bytes + (off < last ? off : last), buf + 64 * j * 16);
             }
             if (it == iters - 1 && straddle) {
                 // piece tl/16 of each row: at most one per lane (PR is not a

@@ -219,6 +219,26 @@ __device__ __forceinline__ void vkf_load_lds16(const void *src, const void *lds)
                  : "memory", "m0");
 }
 
+// ---- streamed weights: loads with the non-temporal cache policy (nt) ----
+// Contiguous runs read exactly once (the GEMV weight regions fetched into
+// LDS) are loaded with nt set.  A plain read of 39.8 MB (640 MB) on MI355X
+// takes 7.60 (102.3) us with default-policy loads and 7.02 (92.7) us with nt
+// loads, the same gain with direct-to-LDS loads (7.89 -> 7.37 us); sc0 / sc1
+// add nothing to nt.  Register loads of 16-byte pieces that neighbouring
+// lanes' pieces share lines with measured slower with nt (Q8_0 4096x4096
+// GEMV 6.7 -> 9.7 us): the policy drops a line before its other pieces are
+// read.
+__device__ __forceinline__ void vkf_load_lds16_nt(const void *src, const void *lds) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(base)
+                 : "memory", "m0");
+}
+template <class T>
+__device__ __forceinline__ T vkf_ld_nt(const void *p) {
+    return __builtin_nontemporal_load((const T *)p);
+}
+
 // ---- wavefront reductions (64 lanes) ----
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
