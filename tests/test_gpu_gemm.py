@@ -30,6 +30,23 @@ def test_linear_fp16_fp32out(dev, M, N, K, transA, transB):
     assert rel_err(D.cpu().numpy(), ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 136, 192), (17, 520, 1024), (300, 1000, 128),
+                                   (1, 4096, 4096), (33, 8, 64)])
+def test_linear_fp16_nn_transposed_reads(dev, M, N, K):
+    """B stored [K, N] (NN, torch.mm(a, b)) with N % 8 == 0 and K % 64 == 0:
+    the B tile is copied to LDS as it lies and read back transposed
+    (ds_read_b64_tr_b16); ragged M and N, one K step, N below one tile."""
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_FP16_FP32OUT
+    rng = np.random.default_rng(seed_for(4, 45) + M + N + K)
+    A, B = _f16(rng, M, K), _f16(rng, K, N)
+    D = ops.linear(to_dev(A, dev), to_dev(B, dev), M, N, K, DTYPE_FP16_FP32OUT, transA=0, transB=0)
+    torch.cuda.synchronize()
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    assert rel_err(D.cpu().numpy(), ref) <= TOL_F32
+
+
 @pytest.mark.parametrize("act", [0, 1, 2, 3])
 def test_linear_fp16_epilogue(dev, act):
     """fp16 out with alpha, beta*C and every activation."""

@@ -1021,6 +1021,103 @@ __device__ __forceinline__ void gemm_mainloop_qdma(const VkfGemmArgs &a, uint32_
     }
 }
 
+// fp16 Y stored [K, C] (an NN product's B [K, N]; torch.mm(a, b) with a
+// contiguous b) with both operands on direct-to-LDS loads: Y's tile is
+// copied as it lies, 64 k-rows of 128 columns (256 bytes each), and the
+// MFMA operand (8 consecutive k of one column per lane) is read back with
+// ds_read_b64_tr_b16.  That instruction works on groups of 16 lanes: with
+// R[s][e] the e-th 16-bit element at lane s's address, lane j receives
+// R[4e + (j >> 2)][j & 3], e = 0..3 (measured on MI355X).  So lane s of a
+// group points at row k0 + (s >> 2), columns 4(s & 3) .. +3 of a 16-column
+// block, and lane j gets column j, rows k0 .. k0+3; two such reads make the
+// 8 k of lane (column j, k-slice g) for the 16x16x32 MFMA.  Row k's 16-byte
+// piece p sits at slot p ^ 2(k & 3) (the direct loads fetch piece
+// slot ^ 2(k & 3) into each slot), so the 4 rows of a 16-lane read fall on
+// different banks.  Needs C % 8 == 0 (no piece straddles the last column),
+// 16-byte aligned Y and row pitch, K % 64 == 0.
+__device__ __forceinline__ bool dma_trb_ok(const void *P, uint64_t ld, uint32_t C, uint32_t K) {
+    return ((ld * 2) % 16) == 0 && (((uintptr_t)P & 15) == 0) && (C % 8) == 0 && (K % 64) == 0;
+}
+
+typedef short vkf_s4 __attribute__((ext_vector_type(4)));
+
+// 4 k of one column: the ds_read_b64_tr_b16 of this lane's address p (LDS)
+__device__ __forceinline__ vkf_i2 lds_read_tr16(const uint8_t *p) {
+    const vkf_s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) vkf_s4 *)(p));
+    return __builtin_bit_cast(vkf_i2, v);
+}
+
+// One 64-k step of the wave's 64x64 tile: X fragments as mfma_step_swz,
+// Y fragments by transposed reads of the [k][column] tile ly.
+template <class ACC>
+__device__ __forceinline__ void mfma_step_trb(const uint8_t *lx, const uint8_t *ly, int wr, int wc, ACC acc[4][4]) {
+    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4, sw = li & 7;
+    const int rsub = li >> 2, hb = (li & 1) * 8;  // this lane's row in a 4-row read, half of its piece
+    vkf_i4 fa[2][4], fb[2][4];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int c = 4 * s + lg;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            fa[s][i] = *(const vkf_i4 *)(lx + (wr * 64 + 16 * i + li) * 128 + ((c ^ sw) << 4));
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int slot = (8 * wc + 2 * j + ((li & 3) >> 1)) ^ (2 * rsub);
+            const uint8_t *q = ly + (32 * s + 8 * lg + rsub) * 256 + slot * 16 + hb;
+            const vkf_i2 lo = lds_read_tr16(q), hi = lds_read_tr16(q + 4 * 256);
+            fb[s][j] = vkf_i4{lo[0], lo[1], hi[0], hi[1]};
+        }
+    }
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = mfma_frag<2>(fa[s][i], fb[s][j], acc[i][j]);
+    __builtin_amdgcn_s_setprio(0);
+}
+
+template <class ACC>
+__device__ __forceinline__ void gemm_mainloop_dma_trb(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, ACC acc[4][4],
+                                                      uint8_t *smem) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wr = wave >> 1, wc = wave & 1;
+    const uint32_t nk = a.K / 64;
+    const uint8_t *gx[4], *gy[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t rr = (4 * wave + j) * 8 + (lane >> 3);
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t rx = r0 + rr < a.R ? r0 + rr : a.R - 1;  // rows past the edge: any valid row
+        gx[j] = (const uint8_t *)a.X + (uint64_t)rx * a.ldx * 2 + ch * 16;
+        // k-row kr of the step, slot lane & 15: columns of piece slot ^ 2(kr & 3)
+        const uint32_t kr = 16 * wave + 4 * j + (lane >> 4), p = (lane & 15) ^ (2 * (kr & 3));
+        const uint32_t col = c0 + 8 * p < a.Cn ? c0 + 8 * p : a.Cn - 8;  // pieces past the edge: any valid one
+        gy[j] = (const uint8_t *)a.Y + ((uint64_t)kr * a.ldy + col) * 2;
+    }
+    const uint64_t ystep = (uint64_t)64 * a.ldy * 2;
+    auto issue = [&](uint32_t kt, uint32_t stage) {
+        uint8_t *sx = smem + stage * 32768, *sy = sx + 16384;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            vkf_load_lds16(gx[j] + (uint64_t)kt * 128, sx + (4 * wave + j) * 8 * 128);
+            vkf_load_lds16(gy[j] + kt * ystep, sy + (16 * wave + 4 * j) * 256);
+        }
+    };
+#pragma unroll
+    for (uint32_t s = 0; s + 1 < GNST; s++)
+        if (s < nk) issue(s, s);
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        if (kt + GNST - 2 < nk) wait_vm<8 * (GNST - 2)>();
+        else wait_vm<0>();
+        __syncthreads();
+        if (kt + GNST - 1 < nk) issue(kt + GNST - 1, (kt + GNST - 1) % GNST);
+        const uint8_t *lx = smem + (kt % GNST) * 32768;
+        mfma_step_trb(lx, lx + 16384, wr, wc, acc);
+    }
+    __syncthreads();  // LDS free for the epilogue
+}
+
 // Dense X K-contiguous (direct-to-LDS tiles) and Y transposed (stored
 // [K, C], e.g. B [K, N] of an NN product, torch.mm(a, b) with contiguous b):
 // Y's 16-byte row pieces come from load_dense_t (loads along Y's contiguous
@@ -1247,6 +1344,8 @@ __device__ __forceinline__ void gemm_f16_body(const VkfGemmArgs &a) {
     if constexpr (XQT < 0 && QT < 0) {
         if (dma_ok(a.X, a.ldx, (a.flags & VKF_GF_X_TRANS) != 0, a.K, 2)) {
             if (dma_ok(a.Y, a.ldy, (a.flags & VKF_GF_Y_TRANS) != 0, a.K, 2)) gemm_mainloop_dma<2>(a, r0, c0, acc, smem);
+            else if ((a.flags & VKF_GF_Y_TRANS) && dma_trb_ok(a.Y, a.ldy, a.Cn, a.K))
+                gemm_mainloop_dma_trb(a, r0, c0, acc, smem);
             else if (a.flags & VKF_GF_Y_TRANS) gemm_mainloop_tdma<2>(a, r0, c0, acc, smem);
             else goto general;
             epilogue_tile(a, r0, c0, acc, smem);
