@@ -47,6 +47,36 @@ def test_linear_fp16_nn_transposed_reads(dev, M, N, K):
     assert rel_err(D.cpu().numpy(), ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 136, 96), (16, 8, 32), (17, 520, 1024), (32, 4096, 4096),
+                                   (33, 200, 4128), (64, 1000, 256)])
+@pytest.mark.parametrize("transB", [1, 0])
+def test_linear_fp16_skinny(dev, M, N, K, transB):
+    """At most 64 rows of A: the skinny kernel (B streamed once by 16-column
+    workgroups, K split over 16 waves, partial tiles summed in wave order),
+    B [N, K] or [K, N]; fp32 out, then fp16 out with alpha, beta*C and an
+    activation, checked against the same float64 product."""
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_FP16, DTYPE_FP16_FP32OUT
+    rng = np.random.default_rng(seed_for(4, 47) + M + N + K + transB)
+    A = _f16(rng, M, K)
+    B = _f16(rng, N, K) if transB else _f16(rng, K, N)
+    Bm = B.T if transB else B
+    ref = A.astype(np.float64) @ Bm.astype(np.float64)
+    D = ops.linear(to_dev(A, dev), to_dev(B, dev), M, N, K, DTYPE_FP16_FP32OUT, transB=transB)
+    torch.cuda.synchronize()
+    assert rel_err(D.cpu().numpy(), ref) <= TOL_F32
+    D2 = ops.linear(to_dev(A, dev), to_dev(B, dev), M, N, K, DTYPE_FP16_FP32OUT, transB=transB)
+    torch.cuda.synchronize()
+    assert bits_equal(D.cpu().numpy(), D2.cpu().numpy())  # fixed summation order
+    C = _f16(rng, M, N)
+    E = ops.linear(to_dev(A, dev), to_dev(B, dev), M, N, K, DTYPE_FP16, transB=transB, act=1,
+                   C=to_dev(C, dev), alpha=0.5, beta=0.25)
+    torch.cuda.synchronize()
+    pre = (0.5 * ref + 0.25 * C.astype(np.float64)).astype(np.float32)
+    assert rel_err(E.cpu().numpy().astype(np.float32), O.np_act(1, pre)) <= TOL_F16
+
+
 @pytest.mark.parametrize("act", [0, 1, 2, 3])
 def test_linear_fp16_epilogue(dev, act):
     """fp16 out with alpha, beta*C and every activation."""

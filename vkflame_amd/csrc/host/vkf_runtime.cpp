@@ -170,10 +170,25 @@ static bool dma_operand(const void *p, uint64_t ld, bool trans, uint32_t K, uint
     return !trans && (ld * es) % 16 == 0 && ((uintptr_t)p & 15) == 0 && ((uint64_t)K * es) % 128 == 0;
 }
 
+// The skinny fp16 kernel's conditions (gemm_skinny in kernels/gemm.hip):
+// X K-contiguous with 16-byte rows, K % 32 == 0, Y 16-byte aligned with
+// 16-byte rows (NT) or rows of C % 8 == 0 columns (NN).
+static bool skinny_ok(const VkfGemmArgs &g, uint32_t batch) {
+    if (g.R > 64 || (g.flags & (VKF_GF_X_TRANS | VKF_GF_X_F16Q)) || g.bpx) return false;
+    if (batch > 1 && ((g.bsx | g.bsy) & 15) != 0) return false;
+    if ((g.ldx * 2) % 16 != 0 || ((uintptr_t)g.X & 15) != 0 || g.K % 32 != 0) return false;
+    if ((g.ldy * 2) % 16 != 0 || ((uintptr_t)g.Y & 15) != 0) return false;
+    return !(g.flags & VKF_GF_Y_TRANS) || g.Cn % 8 == 0;
+}
+
 hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream, uint32_t batch) {
     if (g.R == 0 || g.Cn == 0 || batch == 0) return hipSuccess;
     dim3 grid((g.Cn + 127) / 128, (g.R + 127) / 128, batch);
     if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
+    // at most 64 rows: Y streamed once by 16-column workgroups
+    if (id == VKF_K_GEMM_F16 && skinny_ok(g, batch))
+        return launch(VKF_K_GEMM_F16_SKINNY, dim3((g.Cn + 15) / 16, 1, batch), dim3(1024), &g, sizeof(g), stream,
+                      131072);
     // the split-K kernels need operands the direct-to-LDS loads take, checked
     // here on the host: not for per-batch pointer arrays, which live on the device
     if ((id == VKF_K_GEMM_F16 || id == VKF_K_GEMM_I8) && !(g.flags & VKF_GF_X_F16Q) && !g.bpx &&

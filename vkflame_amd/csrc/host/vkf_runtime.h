@@ -118,6 +118,7 @@
     X(GEMM_I8, "vkf_gemm_i8")                               \
     X(GEMM_F16_K2, "vkf_gemm_f16_k2")                       \
     X(GEMM_I8_K2, "vkf_gemm_i8_k2")                         \
+    X(GEMM_F16_SKINNY, "vkf_gemm_f16_skinny")               \
     /* GEMM: fp16 and Q8_1 activations per weight type */   \
     X(GEMM_Q4_0_F16, "vkf_gemm_q4_0_f16")                   \
     X(GEMM_Q4_0_Q81, "vkf_gemm_q4_0_q8_1")                  \

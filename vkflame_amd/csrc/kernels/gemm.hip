@@ -2029,3 +2029,163 @@ VKF_GEMM_Q_K2(q5_0, VKF_Q5_0)
 VKF_GEMM_Q_K2(q4_k, VKF_Q4_K)
 VKF_GEMM_Q_K2(q5_k, VKF_Q5_K)
 VKF_GEMM_Q_K2(q6_k, VKF_Q6_K)
+
+// ---------------------------------------------------------------------------
+// Skinny fp16 GEMM: at most 64 rows of X (decode-sized batches, torch.mm of
+// a few rows).  So few rows give a 128-row tile nothing to reuse: the kernel
+// is a stream of Y at HBM speed with the rows of X alongside.  One 1024-
+// thread workgroup per 16 columns of Y; its 16 waves split K in 32-k steps,
+// each wave accumulating 16 columns x up to 64 rows on 16x16x32 MFMAs, and
+// the 16 partial tiles are summed in LDS in wave order (a fixed order: the
+// result is repeatable).  Per step a lane loads its 16 bytes of X straight
+// from global memory (rows past R: zero operands, no load) and its B
+// fragment:
+//   Y stored [C, K] (NT): Y[c0 + j][32t + 8g .. +7], one 16-byte load;
+//   Y stored [K, C] (NN): the step's 32 k-rows x 16 columns (32 bytes each)
+//     go to the wave's LDS by one direct load (lane L: row L/2, columns
+//     8(L&1) ..), read back as the fragment by two ds_read_b64_tr_b16 (the
+//     lane layout of mfma_step_trb; 32-byte rows fall on distinct banks).
+// A wave loads CH steps, then multiplies them; 16 waves per CU keep the
+// loads of the others in flight meanwhile.  Workgroups b, b+8, b+16, ...
+// share an XCD and take consecutive column tiles, so tiles that share Y's
+// lines (NN: four per 128-byte line) share that XCD's L2.  Conditions
+// (host): X K-contiguous, 16-byte aligned, ldx % 8 == 0; K % 32 == 0; Y
+// 16-byte aligned with ldy % 8 == 0, and C % 8 == 0 for NN.
+// ---------------------------------------------------------------------------
+#define SK_WAVES 16
+
+__device__ __forceinline__ float epi_one(const VkfGemmArgs &a, uint32_t r, uint32_t c, float v) {
+    // the per-value epilogue of epi_stage, in the same order
+    if (a.rs) v *= a.rs[(a.flags & VKF_GF_RS_SCALAR) ? 0 : r];
+    if (a.cs) v *= a.cs[(a.flags & VKF_GF_CS_SCALAR) ? 0 : c];
+    v *= a.alpha;
+    if (a.beta != 0.0f) {
+        const float cin = (a.flags & VKF_GF_CIN_F32) ? ((const float *)a.Cin)[(uint64_t)r * a.ldc + c]
+                                                     : (float)((const _Float16 *)a.Cin)[(uint64_t)r * a.ldc + c];
+        v = fmaf(a.beta, cin, v);
+    }
+    if (a.bias) {
+        const uint32_t bi = (a.flags & VKF_GF_BIAS_ROW) ? r : c;
+        v += (a.flags & VKF_GF_BIAS_F32) ? ((const float *)a.bias)[bi] : (float)((const _Float16 *)a.bias)[bi];
+    }
+    return vkf_act(a.act, v);
+}
+
+template <int MB, bool YT>
+__device__ __forceinline__ void gemm_skinny(const VkfGemmArgs &a, uint8_t *smem) {
+    constexpr int CH = MB <= 2 ? 8 : 4;  // 32-k steps per load batch
+    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint32_t tile = blockIdx.x;
+    {
+        const uint32_t per = gridDim.x / 8;
+        if (blockIdx.x < per * 8) tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    }
+    const uint32_t c0 = tile * 16;
+    const uint32_t ns = a.K / 32, s0 = wave * ns / SK_WAVES, s1 = (wave + 1) * ns / SK_WAVES;
+
+    const uint8_t *xrow[MB];
+    bool xlive[MB];
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        const uint32_t r = 16 * m + li;
+        xlive[m] = r < a.R;
+        xrow[m] = (const uint8_t *)a.X + (uint64_t)(xlive[m] ? r : 0) * a.ldx * 2 + 16 * lg;
+    }
+    const uint8_t *yp;
+    uint64_t ystep;  // bytes per 32-k step
+    if constexpr (YT) {
+        const uint32_t col = c0 + 8 * (lane & 1) < a.Cn ? c0 + 8 * (lane & 1) : a.Cn - 8;  // past the edge: any valid
+        yp = (const uint8_t *)a.Y + ((uint64_t)(lane >> 1) * a.ldy + col) * 2;
+        ystep = (uint64_t)32 * a.ldy * 2;
+    } else {
+        const uint32_t c = c0 + li < a.Cn ? c0 + li : a.Cn - 1;
+        yp = (const uint8_t *)a.Y + (uint64_t)c * a.ldy * 2 + 16 * lg;
+        ystep = 64;
+    }
+    uint8_t *ring = smem + wave * CH * 1024;  // NN: this wave's staged steps
+    const int rsub = li >> 2, hb = (li & 1) * 8, pcol = ((li & 3) >> 1) * 16;
+
+    vkf_f4 acc[MB];
+#pragma unroll
+    for (int m = 0; m < MB; m++) acc[m] = vkf_f4{0, 0, 0, 0};
+    for (uint32_t t0 = s0; t0 < s1; t0 += CH) {  // wave-uniform
+        const uint32_t n = s1 - t0 < CH ? s1 - t0 : CH;
+        vkf_i4 xa[CH][MB], yb[CH];
+        if constexpr (YT) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the ring's previous reads are done
+#pragma unroll
+            for (int q = 0; q < CH; q++)
+                if (q < (int)n) vkf_load_lds16_nt(yp + (t0 + q) * ystep, ring + q * 1024);
+        }
+#pragma unroll
+        for (int q = 0; q < CH; q++) {
+            if (q < (int)n) {
+                if constexpr (!YT) yb[q] = *(const vkf_i4 *)(yp + (t0 + q) * ystep);
+#pragma unroll
+                for (int m = 0; m < MB; m++)
+                    xa[q][m] = xlive[m] ? *(const vkf_i4 *)(xrow[m] + (uint64_t)(t0 + q) * 64) : vkf_i4{0, 0, 0, 0};
+            }
+        }
+        if constexpr (YT) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int q = 0; q < CH; q++) {
+            if (q < (int)n) {
+                vkf_i4 fb;
+                if constexpr (YT) {
+                    // rows 8g + 4h + (li >> 2) of the step, columns 4(li & 3) ..
+                    const uint8_t *p = ring + q * 1024 + (8 * lg + rsub) * 32 + pcol + hb;
+                    const vkf_i2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * 32);
+                    fb = vkf_i4{lo[0], lo[1], hi[0], hi[1]};
+                } else {
+                    fb = yb[q];
+                }
+#pragma unroll
+                for (int m = 0; m < MB; m++) acc[m] = mfma_frag<2>(xa[q][m], fb, acc[m]);
+            }
+        }
+    }
+    // partial tiles of the 16 waves summed in wave order
+    __syncthreads();
+    float *red = (float *)smem;  // [wave][m][lane][4]
+#pragma unroll
+    for (int m = 0; m < MB; m++) *(vkf_f4 *)(red + ((wave * MB + m) * 64 + lane) * 4) = acc[m];
+    __syncthreads();
+    if (wave < MB) {
+        const int m = wave;
+        vkf_f4 s = *(const vkf_f4 *)(red + (m * 64 + lane) * 4);
+        for (int w = 1; w < SK_WAVES; w++) {
+            const vkf_f4 v = *(const vkf_f4 *)(red + ((w * MB + m) * 64 + lane) * 4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) s[e] += v[e];
+        }
+        const uint32_t c = c0 + li;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t r = 16 * m + 4 * lg + e;
+            if (r < a.R && c < a.Cn) {
+                const float v = epi_one(a, r, c, s[e]);
+                if (a.flags & VKF_GF_D_F32) ((float *)a.D)[(uint64_t)r * a.ldd + c] = v;
+                else ((_Float16 *)a.D)[(uint64_t)r * a.ldd + c] = vkf_to_f16(v);
+            }
+        }
+    }
+}
+
+// LDS: the NN staging ring (16 waves x CH KiB) or the partial tiles
+// (16 waves x MB KiB), the larger: 128 KiB
+VKF_KERNEL void __launch_bounds__(64 * SK_WAVES) vkf_gemm_f16_skinny(VkfGemmArgs a0) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sk_smem[];
+    const VkfGemmArgs a = gemm_batch(a0);
+    const bool yt = (a.flags & VKF_GF_Y_TRANS) != 0;
+    if (a.R <= 16) {
+        if (yt) gemm_skinny<1, true>(a, sk_smem);
+        else gemm_skinny<1, false>(a, sk_smem);
+    } else if (a.R <= 32) {
+        if (yt) gemm_skinny<2, true>(a, sk_smem);
+        else gemm_skinny<2, false>(a, sk_smem);
+    } else {
+        if (yt) gemm_skinny<4, true>(a, sk_smem);
+        else gemm_skinny<4, false>(a, sk_smem);
+    }
+}
