@@ -229,6 +229,42 @@ def run_suite(torch, ops, O, replays, only=None):
                   [(lambda c=c: ops.gemm_q(c, O.Q6_K, xq, N, K, out=y)) for c in copies])
         del w, copies, xf, xq, y
         torch.cuda.empty_cache()
+    # dense fp16 linear (vkflame_dispatch_linear / hipblasGemmEx): the M = 512
+    # FFN shape, and the six torch.mm shapes of the reference's only published
+    # run (added-files/Test-Run-RCOM-Vulkan.md:22-27; torch.mm(a, b) with a
+    # contiguous b is B [K, N], the NN layout), B rotated through cold copies;
+    # torch.mm on the same inputs (ROCm's library) timed beside for context
+    from vkflame_amd._lib import DTYPE_FP16
+    dense = [("fp16 linear 512x5120x5120 NT (B [N, K])", 512, 5120, 5120, 1)]
+    dense += [(f"fp16 torch.mm ({m},{k},{n}) NN (B [K, N])", m, n, k, 0)
+              for (m, k, n) in ((256, 256, 256), (1024, 1024, 1024), (4096, 4096, 4096), (1, 4096, 4096),
+                                (32, 4096, 4096), (128, 8192, 8192))]
+    for (name, M, N, K, tb) in dense:
+        if not want(name):
+            continue
+        rng = np.random.default_rng(_seed(6, M + N + K + tb))
+        a = torch.from_numpy(rng.normal(0, 1, (M, K)).astype(np.float16)).to(dev)
+        b = torch.from_numpy(rng.normal(0, 1, (N, K) if tb else (K, N)).astype(np.float16)).to(dev)
+        copies = _rotating_copies(torch, b, b.numel() * 2)
+        d = torch.empty((M, N), dtype=torch.float16, device=dev)
+        nl = max(32, len(copies))
+        fl = 2.0 * M * N * K
+        ms = median(time_graph(torch, [(lambda c=copies[i % len(copies)]: ops.linear(a, c, M, N, K, DTYPE_FP16,
+                                                                                      transB=tb, out=d))
+                                       for i in range(nl)], max(5, replays // 4)))
+        bt = [c.t() if tb else c for c in copies]  # torch.mm(a, B) with B [K, N]
+        ms_t = median(time_graph(torch, [(lambda c=bt[i % len(bt)]: torch.mm(a, c, out=d)) for i in range(nl)],
+                                 max(5, replays // 4)))
+        t = fl / (ms * 1e-3) / 1e12
+        line = {"config": name, "kernel_us": round(ms * 1e3, 2), "TOPS": round(t, 2),
+                "mfma_frac": round(t / FP16_PEAK_TFLOPS, 4), "peak_TOPS": FP16_PEAK_TFLOPS, "peak": "fp16 dense MFMA",
+                "B_GBps": round(b.numel() * 2 / (ms * 1e-3) / 1e9, 1),
+                "hbm_frac_B": round(b.numel() * 2 / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "torch_mm_us": round(ms_t * 1e3, 2), "weight_copies": len(copies)}
+        log(json.dumps(line))
+        out.append(line)
+        del a, b, copies, bt, d
+        torch.cuda.empty_cache()
     return out
 
 
