@@ -69,6 +69,34 @@ def test_gemm_ex_fp16(dev, L, handle, opA, opB, ctype):
     assert np.array_equal(got[:, m:], C0[:, m:])      # ld padding untouched
 
 
+@pytest.mark.parametrize("m,n,k", [(256, 96, 128), (136, 40, 96), (200, 33, 64)])
+def test_gemm_strided_batched_fp16_nn_aligned(dev, L, handle, m, n, k):
+    """Both ops N with aligned leading dimensions (torch.mm's call): B
+    column-major k x n is the K-contiguous operand and A column-major m x k
+    the [K, M] one, read back through ds_read_b64_tr_b16; n <= 64 takes the
+    skinny kernel.  Three batches with strides of whole 16-byte pieces, fp32
+    C with alpha and beta."""
+    import torch
+    nb = 3
+    rng = np.random.default_rng(seed_for(4, 85) + m + n + k)
+    A = rng.normal(0, 1, (nb, k, m)).astype(np.float16)    # column j of A (m x k, lda = m) at A[b, j]
+    Bm = rng.normal(0, 1, (nb, n, k)).astype(np.float16)   # column j of B (k x n, ldb = k) at Bm[b, j]
+    C0 = rng.normal(0, 1, (nb, n, m)).astype(np.float32)   # column j of C (m x n, ldc = m) at C0[b, j]
+    tA, tB, tC = to_dev(A, dev), to_dev(Bm, dev), to_dev(C0, dev)
+    al, be = ctypes.c_float(0.75), ctypes.c_float(-0.5)
+    st = L.hipblasGemmStridedBatchedEx(handle, B.OP_N, B.OP_N, m, n, k, ctypes.byref(al), _ptr(tA), B.R_16F, m,
+                                       m * k, _ptr(tB), B.R_16F, k, n * k, ctypes.byref(be), _ptr(tC), B.R_32F, m,
+                                       n * m, nb, B.COMPUTE_32F, B.GEMM_DEFAULT)
+    assert st == B.ST_SUCCESS
+    torch.cuda.synchronize()
+    got = tC.cpu().numpy()
+    for b in range(nb):
+        opa = A[b].T.astype(np.float64)                      # m x k
+        opb = Bm[b].T.astype(np.float64)                     # k x n
+        ref = 0.75 * (opa @ opb) - 0.5 * C0[b].T.astype(np.float64)
+        assert rel_err(got[b].T, ref) <= TOL_F32
+
+
 def test_gemm_ex_int8_int32(dev, L, handle):
     import torch
     m, n, k = 257, 129, 320
