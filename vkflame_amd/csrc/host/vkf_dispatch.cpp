@@ -250,6 +250,18 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
         const bool m1_ok = mf == 6 && cdiv(N, 16) >= 2u * (uint32_t)vkf::cu_count();
         if (mf >= 0 && mf_ok && (M >= 2 || m1_ok) && (K % 256) == 0 && aligned(w, ga) && (row_bytes % ga) == 0 &&
             vkf::max_lds() >= kMfmaRed + per_group) {
+            // fp16 activations in registers (gemv_mfma_xr: P waves split K,
+            // each holding its 256-k groups' activations for the launch, no
+            // LDS image): Q4_0 / Q4_1 with K <= 4096 on 16 waves (one group
+            // each; 11008x4096 M = 16 17.1 -> 12.1 us, M = 4 12.2 -> 11.4),
+            // Q4_K with K <= 5120 on 10 waves (two groups each)
+            const bool xr01 = (mf == 1 || mf == 2) && K <= 4096, xrk = mf == 0 && K <= 5120;
+            if (xk == 0 && (xr01 || xrk)) {
+                const uint32_t tiles = cdiv(N, 16), cus = (uint32_t)vkf::cu_count(), P = xrk ? 10 : 16;
+                const VkfKernelId k = xrk ? VKF_K_GEMV_MFMA_XR_Q4_K_F16_P10
+                                          : mf == 1 ? VKF_K_GEMV_MFMA_XR_Q4_0_F16 : VKF_K_GEMV_MFMA_XR_Q4_1_F16;
+                return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * P), a, S(stream), 1024 * P);
+            }
             const uint32_t nsb = (uint32_t)(K / 256), cap = (uint32_t)((vkf::max_lds() - kMfmaRed) / per_group);
             const uint32_t slices = cdiv(nsb, cap), per = cdiv(nsb, slices);
             const uint32_t cus = (uint32_t)vkf::cu_count(), tiles = cdiv(N, 16);

@@ -493,6 +493,197 @@ __device__ __forceinline__ vkf_h8 gm_decode_q6(uint32_t d0, uint32_t d1, uint32_
     return __builtin_bit_cast(vkf_h8, r);
 }
 
+// One 256-k group of one 16-row tile: y4 += the group's products.  X(t)
+// gives the activation operand of MFMA step t (8 fp16, the decode's k
+// order) and XM() the min-term operand of Q4_K / Q5_K (the sub-block sums
+// of x on even k-slices, zero on odd ones).
+template <int F, class XF, class XMF>
+__device__ __forceinline__ void gm_group(const GmSb<F> &T, XF X, XMF XM, int lg, uint32_t sel, uint32_t c64,
+                                         vkf_f4 &y4) {
+    const vkf_f4 zero = {0, 0, 0, 0};
+    const vkf_h2 one16 = {(_Float16)1.0f, (_Float16)0.0625f}, off = {(_Float16)-1024.0f, (_Float16)-64.0f};
+    const vkf_h2 m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    (void)XM;
+    (void)sel;
+    (void)one16;
+    (void)off;
+    (void)m1024;
+    if constexpr (F == GF_Q6_K) {
+        uint32_t w[5][4];  // the runs, shifted into place
+#pragma unroll
+        for (int k = 0; k < 5; k++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                w[k][c] = __builtin_amdgcn_alignbyte(c < 3 ? T.r[k][c + 1] : T.e[k], T.r[k][c], T.sh);
+        const uint32_t qs = 2u * (lg >> 1);  // + 4h
+        vkf_f4 acc = zero;
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int8_t scb = (int8_t)(w[4][2 * n + h] >> (8 * lg));
+                const _Float16 sc = (_Float16)(float)scb;
+                const vkf_h2 sc2 = {sc, sc};
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    const vkf_h8 xv = X(4 * n + 2 * h + hf);
+                    const uint32_t d0 = w[n][2 * hf], d1 = w[n][2 * hf + 1];
+                    const uint32_t e0 = w[2 + n][2 * hf], e1 = w[2 + n][2 * hf + 1];
+                    const vkf_h8 bv = h ? gm_decode_q6<1>(d0, d1, e0, e1, qs + 4, sc2, c64)
+                                        : gm_decode_q6<0>(d0, d1, e0, e1, qs, sc2, c64);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, bv, acc, 0, 0, 0);
+                }
+            }
+        const float d = vkf_h2f(T.d);
+#pragma unroll
+        for (int e = 0; e < 4; e++) y4[e] = fmaf(d, acc[e], y4[e]);
+    } else if constexpr (F == GF_Q5_0) {
+        // block 0: d at bytes 0-1, qh 2 .. 5, qs 6 .. 21; block 1: d at 22-23,
+        // qh 24 .. 27, qs 28 .. 43 (dwords w[k] = bytes 4k .. 4k+3)
+        
+        const uint32_t w[11] = {T.v[0][0], T.v[0][1], T.v[0][2], T.v[0][3], T.v[1][0], T.v[1][1],
+                                T.v[1][2], T.v[1][3], T.v[2][1], T.v[2][2], T.v[2][3]};
+        uint32_t q[2][4], qh[2], dd[2];
+        dd[0] = w[0] & 0xffffu;
+        qh[0] = __builtin_amdgcn_alignbyte(w[1], w[0], 2);
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[0][k] = __builtin_amdgcn_alignbyte(w[k + 2], w[k + 1], 2);
+        dd[1] = w[5] >> 16;
+        qh[1] = w[6];
+        q[1][0] = w[7]; q[1][1] = w[8]; q[1][2] = w[9]; q[1][3] = w[10];
+#pragma unroll
+        for (int blk = 0; blk < 2; blk++) {
+            const _Float16 d = gm_f16(dd[blk]);
+            const vkf_h2 d2 = {d, d};
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                const uint32_t c0 = q[blk][2 * hf], c1 = q[blk][2 * hf + 1];
+                // steps 4blk + hf (elements 8hf .. +7, low nibbles) and 4blk + 2 + hf (16 + 8hf .., high)
+                const vkf_h8 xl = X(4 * blk + hf);
+                const vkf_h8 xh = X(4 * blk + hf + 2);
+                const uint32_t el = 8 * hf, eh = 16 + 8 * hf;
+                const vkf_h8 bl = gm_decode_q50<0>(c0, c1, gm_spread4(qh[blk], el), gm_spread4(qh[blk], el + 4), d2, c64);
+                const vkf_h8 bh = gm_decode_q50<1>(c0, c1, gm_spread4(qh[blk], eh), gm_spread4(qh[blk], eh + 4), d2, c64);
+                y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, y4, 0, 0, 0);
+                y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, y4, 0, 0, 0);
+            }
+        }
+    } else if constexpr (F == GF_Q8_0) {
+        // block 0: d at bytes 0-1, codes 2 .. 33; block 1: d at 34-35, codes 36 .. 67
+        
+        const uint32_t w[17] = {T.v[0][0], T.v[0][1], T.v[0][2], T.v[0][3], T.v[1][0], T.v[1][1],
+                                T.v[1][2], T.v[1][3], T.v[2][0], T.v[2][1], T.v[2][2], T.v[2][3],
+                                T.v[3][0], T.v[3][1], T.v[3][2], T.v[3][3], T.e};
+#pragma unroll
+        for (int blk = 0; blk < 2; blk++) {
+            const _Float16 d = gm_f16(blk ? w[8] >> 16 : w[0] & 0xffffu);
+            const vkf_h2 d2 = {d, d};
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                uint32_t c0, c1;
+                if (blk == 0) {
+                    c0 = __builtin_amdgcn_alignbyte(w[2 * st + 1], w[2 * st], 2);
+                    c1 = __builtin_amdgcn_alignbyte(w[2 * st + 2], w[2 * st + 1], 2);
+                } else {
+                    c0 = w[9 + 2 * st];
+                    c1 = w[10 + 2 * st];
+                }
+                const vkf_h8 xv = X(4 * blk + st);
+                y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, gm_decode_q8(c0, c1, d2, c64), y4, 0, 0,
+                                                            0);
+            }
+        }
+    } else if constexpr (gm_kmin<F>()) {
+        const vkf_u4 hdr = T.v[0];
+        const float dall = vkf_h2f(hdr[0] & 0xffffu), dmin = vkf_h2f(hdr[0] >> 16);
+        const uint32_t s0w = hdr[1], s4w = hdr[2], s8w = hdr[3];
+        const uint32_t sc[2] = {s0w & 0x3f3f3f3fu, (s8w & 0x0f0f0f0fu) | ((s0w >> 2) & 0x30303030u)};
+        const uint32_t mn[2] = {s4w & 0x3f3f3f3fu,
+                                ((s8w >> 4) & 0x0f0f0f0fu) | ((s4w >> 2) & 0x30303030u)};
+        // load L covers sub-blocks 4L + 2h (low nibbles) and 4L + 2h + 1
+        // (high): scale pairs (sc, sc'/16), (-1024 sc, -64 sc'), and
+        // the mins (mn, mn') of those sub-blocks
+        vkf_h2 S[2], Nn[2];
+        uint32_t bm[2];
+#pragma unroll
+        for (int L = 0; L < 2; L++) {
+            S[L] = __builtin_elementwise_fma(gm_h2(__builtin_amdgcn_perm(0x64646464u, sc[L], sel)), one16,
+                                             off);
+            Nn[L] = S[L] * m1024;
+            bm[L] = gm_u(gm_h2(__builtin_amdgcn_perm(0x64646464u, mn[L], sel)) + m1024);
+        }
+        vkf_f4 acc = zero;
+#pragma unroll
+        for (int L = 0; L < 2; L++)
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                const vkf_u4 q = T.v[(F == GF_Q5_K ? 2 : 1) + L];
+                const uint32_t d0 = q[2 * hf], d1 = q[2 * hf + 1], e0 = d0 >> 8, e1 = d1 >> 8;
+                // MFMA steps 8sb + 4L + hf (low nibbles) and 8sb + 4L + 2 + hf (high)
+                const vkf_h8 xl = X(4 * L + hf);
+                const vkf_h8 xh = X(4 * L + hf + 2);
+                vkf_h8 bl, bh;
+                if constexpr (F == GF_Q5_K) {
+                    // sub-blocks 4L + 2(g>>1) (low nibbles) and + 1 (high)
+                    const uint32_t jl = 4 * L + 2 * (lg >> 1);
+                    const uint32_t h0 = T.v[1][2 * hf], h1 = T.v[1][2 * hf + 1];
+                    bl = gm_decode5<0>(d0, e0, d1, e1, h0 >> jl, h1 >> jl, S[L][0], Nn[L][0], c64);
+                    bh = gm_decode5<1>(d0, e0, d1, e1, h0 >> (jl + 1), h1 >> (jl + 1), S[L][1], Nn[L][1],
+                                       c64);
+                } else {
+                    bl = gm_decode<0>(d0, e0, d1, e1, S[L][0], Nn[L][0], c64);
+                    bh = gm_decode<1>(d0, e0, d1, e1, S[L][1], Nn[L][1], c64);
+                }
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, acc, 0, 0, 0);
+            }
+        // min term: even k-slices carry xs hi and lo of the lane pair's 4
+        // sub-blocks, odd ones zero
+        const vkf_h8 xm = XM();
+        const vkf_u4 bmin = {bm[0], bm[1], bm[0], bm[1]};
+        const vkf_f4 am =
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, __builtin_bit_cast(vkf_h8, bmin), zero, 0, 0, 0);
+        const float dm32 = -32.0f * dmin;
+#pragma unroll
+        for (int e = 0; e < 4; e++) y4[e] = fmaf(dm32, am[e], fmaf(dall, acc[e], y4[e]));
+    } else {
+        // block pair 2g, 2g+1: code dwords and (d, m) of each block
+        const vkf_u4 w0 = T.v[0], w1 = T.v[1];
+        uint32_t q[2][4], dm[2];
+        if constexpr (F == GF_Q4_0) {
+            // 18-byte blocks: block 0 = bytes 0..17 (qs from byte 2),
+            // block 1 = bytes 18..35 (qs from byte 20, aligned)
+            const uint32_t w[5] = {w0[0], w0[1], w0[2], w0[3], w1[0]};
+#pragma unroll
+            for (int j = 0; j < 4; j++) q[0][j] = __builtin_amdgcn_alignbyte(w[j + 1], w[j], 2);
+            q[1][0] = w1[1]; q[1][1] = w1[2]; q[1][2] = w1[3]; q[1][3] = T.v[2][0];
+            dm[0] = w0[0] & 0xffffu;
+            dm[1] = w1[0] >> 16;
+        } else {
+            // 20-byte blocks: (d, m), 16 bytes of qs
+            q[0][0] = w0[1]; q[0][1] = w0[2]; q[0][2] = w0[3]; q[0][3] = w1[0];
+            q[1][0] = w1[2]; q[1][1] = w1[3]; q[1][2] = T.v[2][0]; q[1][3] = T.v[2][1];
+            dm[0] = w0[0];
+            dm[1] = w1[1];
+        }
+#pragma unroll
+        for (int blk = 0; blk < 2; blk++) {
+            const _Float16 d = gm_f16(dm[blk] & 0xffffu), m = gm_f16(dm[blk] >> 16);
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                const uint32_t d0 = q[blk][2 * hf], d1 = q[blk][2 * hf + 1];
+                // steps 4blk + hf (low nibbles) and 4blk + 2 + hf (high)
+                const vkf_h8 xl = X(4 * blk + hf);
+                const vkf_h8 xh = X(4 * blk + hf + 2);
+                const vkf_h8 bl = gm_decode_w<F, 0>(d0, d1, d, m, c64);
+                const vkf_h8 bh = gm_decode_w<F, 1>(d0, d1, d, m, c64);
+                y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, y4, 0, 0, 0);
+                y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, y4, 0, 0, 0);
+            }
+        }
+    }
+}
+
 template <int F, uint32_t MR, int XK>
 __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *smem) {
     const uint32_t nsb = a.K / 256;
@@ -537,8 +728,6 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
     const unsigned char *xsw = xs + ((lg >> 1) * MR + arow) * 16;
     const uint32_t sel = (lg >> 1) ? 0x04030402u : 0x04010400u;  // bytes 2h, 2h+1 as (1024 + v) fp16
     const vkf_f4 zero = {0, 0, 0, 0};
-    const vkf_h2 one16 = {(_Float16)1.0f, (_Float16)0.0625f}, off = {(_Float16)-1024.0f, (_Float16)-64.0f};
-    const vkf_h2 m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
     uint32_t c64 = 0x64006400u;
     asm volatile("" : "+v"(c64));  // held in a VGPR for gm_and_or
 
@@ -553,186 +742,13 @@ __device__ __forceinline__ void gemv_mfma(const VkfGemvArgs &a, unsigned char *s
                 const uint32_t sb = s0 + u;
                 if (sb >= sb1) break;
                 const unsigned char *xg = xw + sb * (32 * MR * 16);  // step 8sb
-                if constexpr (F == GF_Q6_K) {
-                    const GmSb<F> &T = tt[u];
-                    uint32_t w[5][4];  // the runs, shifted into place
-#pragma unroll
-                    for (int k = 0; k < 5; k++)
-#pragma unroll
-                        for (int c = 0; c < 4; c++)
-                            w[k][c] = __builtin_amdgcn_alignbyte(c < 3 ? T.r[k][c + 1] : T.e[k], T.r[k][c], T.sh);
-                    const uint32_t qs = 2u * (lg >> 1);  // + 4h
-                    vkf_f4 acc = zero;
-#pragma unroll
-                    for (int n = 0; n < 2; n++)
-#pragma unroll
-                        for (int h = 0; h < 2; h++) {
-                            const int8_t scb = (int8_t)(w[4][2 * n + h] >> (8 * lg));
-                            const _Float16 sc = (_Float16)(float)scb;
-                            const vkf_h2 sc2 = {sc, sc};
-#pragma unroll
-                            for (int hf = 0; hf < 2; hf++) {
-                                const unsigned char *xp = xg + (4 * n + 2 * h + hf) * (4 * MR * 16);
-                                const vkf_h8 xv = *(const vkf_h8 *)xp;
-                                const uint32_t d0 = w[n][2 * hf], d1 = w[n][2 * hf + 1];
-                                const uint32_t e0 = w[2 + n][2 * hf], e1 = w[2 + n][2 * hf + 1];
-                                const vkf_h8 bv = h ? gm_decode_q6<1>(d0, d1, e0, e1, qs + 4, sc2, c64)
-                                                    : gm_decode_q6<0>(d0, d1, e0, e1, qs, sc2, c64);
-                                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, bv, acc, 0, 0, 0);
-                            }
-                        }
-                    const float d = vkf_h2f(T.d);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) y4[e] = fmaf(d, acc[e], y4[e]);
-                } else if constexpr (F == GF_Q5_0) {
-                    // block 0: d at bytes 0-1, qh 2 .. 5, qs 6 .. 21; block 1: d at 22-23,
-                    // qh 24 .. 27, qs 28 .. 43 (dwords w[k] = bytes 4k .. 4k+3)
-                    const GmSb<F> &T = tt[u];
-                    const uint32_t w[11] = {T.v[0][0], T.v[0][1], T.v[0][2], T.v[0][3], T.v[1][0], T.v[1][1],
-                                            T.v[1][2], T.v[1][3], T.v[2][1], T.v[2][2], T.v[2][3]};
-                    uint32_t q[2][4], qh[2], dd[2];
-                    dd[0] = w[0] & 0xffffu;
-                    qh[0] = __builtin_amdgcn_alignbyte(w[1], w[0], 2);
-#pragma unroll
-                    for (int k = 0; k < 4; k++) q[0][k] = __builtin_amdgcn_alignbyte(w[k + 2], w[k + 1], 2);
-                    dd[1] = w[5] >> 16;
-                    qh[1] = w[6];
-                    q[1][0] = w[7]; q[1][1] = w[8]; q[1][2] = w[9]; q[1][3] = w[10];
-#pragma unroll
-                    for (int blk = 0; blk < 2; blk++) {
-                        const _Float16 d = gm_f16(dd[blk]);
-                        const vkf_h2 d2 = {d, d};
-#pragma unroll
-                        for (int hf = 0; hf < 2; hf++) {
-                            const uint32_t c0 = q[blk][2 * hf], c1 = q[blk][2 * hf + 1];
-                            // steps 4blk + hf (elements 8hf .. +7, low nibbles) and 4blk + 2 + hf (16 + 8hf .., high)
-                            const unsigned char *xp = xg + (4 * blk + hf) * (4 * MR * 16);
-                            const vkf_h8 xl = *(const vkf_h8 *)xp;
-                            const vkf_h8 xh = *(const vkf_h8 *)(xp + 2 * (4 * MR * 16));
-                            const uint32_t el = 8 * hf, eh = 16 + 8 * hf;
-                            const vkf_h8 bl = gm_decode_q50<0>(c0, c1, gm_spread4(qh[blk], el), gm_spread4(qh[blk], el + 4), d2, c64);
-                            const vkf_h8 bh = gm_decode_q50<1>(c0, c1, gm_spread4(qh[blk], eh), gm_spread4(qh[blk], eh + 4), d2, c64);
-                            y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, y4, 0, 0, 0);
-                            y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, y4, 0, 0, 0);
-                        }
-                    }
-                } else if constexpr (F == GF_Q8_0) {
-                    // block 0: d at bytes 0-1, codes 2 .. 33; block 1: d at 34-35, codes 36 .. 67
-                    const GmSb<F> &T = tt[u];
-                    const uint32_t w[17] = {T.v[0][0], T.v[0][1], T.v[0][2], T.v[0][3], T.v[1][0], T.v[1][1],
-                                            T.v[1][2], T.v[1][3], T.v[2][0], T.v[2][1], T.v[2][2], T.v[2][3],
-                                            T.v[3][0], T.v[3][1], T.v[3][2], T.v[3][3], T.e};
-#pragma unroll
-                    for (int blk = 0; blk < 2; blk++) {
-                        const _Float16 d = gm_f16(blk ? w[8] >> 16 : w[0] & 0xffffu);
-                        const vkf_h2 d2 = {d, d};
-#pragma unroll
-                        for (int st = 0; st < 4; st++) {
-                            uint32_t c0, c1;
-                            if (blk == 0) {
-                                c0 = __builtin_amdgcn_alignbyte(w[2 * st + 1], w[2 * st], 2);
-                                c1 = __builtin_amdgcn_alignbyte(w[2 * st + 2], w[2 * st + 1], 2);
-                            } else {
-                                c0 = w[9 + 2 * st];
-                                c1 = w[10 + 2 * st];
-                            }
-                            const vkf_h8 xv = *(const vkf_h8 *)(xg + (4 * blk + st) * (4 * MR * 16));
-                            y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, gm_decode_q8(c0, c1, d2, c64), y4, 0, 0,
-                                                                        0);
-                        }
-                    }
-                } else if constexpr (gm_kmin<F>()) {
-                    const vkf_u4 hdr = tt[u].v[0];
-                    const float dall = vkf_h2f(hdr[0] & 0xffffu), dmin = vkf_h2f(hdr[0] >> 16);
-                    const uint32_t s0w = hdr[1], s4w = hdr[2], s8w = hdr[3];
-                    const uint32_t sc[2] = {s0w & 0x3f3f3f3fu, (s8w & 0x0f0f0f0fu) | ((s0w >> 2) & 0x30303030u)};
-                    const uint32_t mn[2] = {s4w & 0x3f3f3f3fu,
-                                            ((s8w >> 4) & 0x0f0f0f0fu) | ((s4w >> 2) & 0x30303030u)};
-                    // load L covers sub-blocks 4L + 2h (low nibbles) and 4L + 2h + 1
-                    // (high): scale pairs (sc, sc'/16), (-1024 sc, -64 sc'), and
-                    // the mins (mn, mn') of those sub-blocks
-                    vkf_h2 S[2], Nn[2];
-                    uint32_t bm[2];
-#pragma unroll
-                    for (int L = 0; L < 2; L++) {
-                        S[L] = __builtin_elementwise_fma(gm_h2(__builtin_amdgcn_perm(0x64646464u, sc[L], sel)), one16,
-                                                         off);
-                        Nn[L] = S[L] * m1024;
-                        bm[L] = gm_u(gm_h2(__builtin_amdgcn_perm(0x64646464u, mn[L], sel)) + m1024);
-                    }
-                    vkf_f4 acc = zero;
-#pragma unroll
-                    for (int L = 0; L < 2; L++)
-#pragma unroll
-                        for (int hf = 0; hf < 2; hf++) {
-                            const vkf_u4 q = tt[u].v[(F == GF_Q5_K ? 2 : 1) + L];
-                            const uint32_t d0 = q[2 * hf], d1 = q[2 * hf + 1], e0 = d0 >> 8, e1 = d1 >> 8;
-                            // MFMA steps 8sb + 4L + hf (low nibbles) and 8sb + 4L + 2 + hf (high)
-                            const unsigned char *xp = xg + (4 * L + hf) * (4 * MR * 16);
-                            const vkf_h8 xl = *(const vkf_h8 *)xp;
-                            const vkf_h8 xh = *(const vkf_h8 *)(xp + 2 * (4 * MR * 16));
-                            vkf_h8 bl, bh;
-                            if constexpr (F == GF_Q5_K) {
-                                // sub-blocks 4L + 2(g>>1) (low nibbles) and + 1 (high)
-                                const uint32_t jl = 4 * L + 2 * (lg >> 1);
-                                const uint32_t h0 = tt[u].v[1][2 * hf], h1 = tt[u].v[1][2 * hf + 1];
-                                bl = gm_decode5<0>(d0, e0, d1, e1, h0 >> jl, h1 >> jl, S[L][0], Nn[L][0], c64);
-                                bh = gm_decode5<1>(d0, e0, d1, e1, h0 >> (jl + 1), h1 >> (jl + 1), S[L][1], Nn[L][1],
-                                                   c64);
-                            } else {
-                                bl = gm_decode<0>(d0, e0, d1, e1, S[L][0], Nn[L][0], c64);
-                                bh = gm_decode<1>(d0, e0, d1, e1, S[L][1], Nn[L][1], c64);
-                            }
-                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, acc, 0, 0, 0);
-                        }
-                    // min term: even k-slices carry xs hi and lo of the lane pair's 4
-                    // sub-blocks, odd ones zero
+                const auto X = [&](int t) { return *(const vkf_h8 *)(xg + t * (4 * MR * 16)); };
+                const auto XM = [&]() {
                     vkf_h8 xm = {};
                     if ((lg & 1) == 0) xm = *(const vkf_h8 *)(xsw + sb * (2 * MR * 16));
-                    const vkf_u4 bmin = {bm[0], bm[1], bm[0], bm[1]};
-                    const vkf_f4 am =
-                        __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, __builtin_bit_cast(vkf_h8, bmin), zero, 0, 0, 0);
-                    const float dm32 = -32.0f * dmin;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) y4[e] = fmaf(dm32, am[e], fmaf(dall, acc[e], y4[e]));
-                } else {
-                    // block pair 2g, 2g+1: code dwords and (d, m) of each block
-                    const vkf_u4 w0 = tt[u].v[0], w1 = tt[u].v[1];
-                    uint32_t q[2][4], dm[2];
-                    if constexpr (F == GF_Q4_0) {
-                        // 18-byte blocks: block 0 = bytes 0..17 (qs from byte 2),
-                        // block 1 = bytes 18..35 (qs from byte 20, aligned)
-                        const uint32_t w[5] = {w0[0], w0[1], w0[2], w0[3], w1[0]};
-#pragma unroll
-                        for (int j = 0; j < 4; j++) q[0][j] = __builtin_amdgcn_alignbyte(w[j + 1], w[j], 2);
-                        q[1][0] = w1[1]; q[1][1] = w1[2]; q[1][2] = w1[3]; q[1][3] = tt[u].v[2][0];
-                        dm[0] = w0[0] & 0xffffu;
-                        dm[1] = w1[0] >> 16;
-                    } else {
-                        // 20-byte blocks: (d, m), 16 bytes of qs
-                        q[0][0] = w0[1]; q[0][1] = w0[2]; q[0][2] = w0[3]; q[0][3] = w1[0];
-                        q[1][0] = w1[2]; q[1][1] = w1[3]; q[1][2] = tt[u].v[2][0]; q[1][3] = tt[u].v[2][1];
-                        dm[0] = w0[0];
-                        dm[1] = w1[1];
-                    }
-#pragma unroll
-                    for (int blk = 0; blk < 2; blk++) {
-                        const _Float16 d = gm_f16(dm[blk] & 0xffffu), m = gm_f16(dm[blk] >> 16);
-#pragma unroll
-                        for (int hf = 0; hf < 2; hf++) {
-                            const uint32_t d0 = q[blk][2 * hf], d1 = q[blk][2 * hf + 1];
-                            // steps 4blk + hf (low nibbles) and 4blk + 2 + hf (high)
-                            const unsigned char *xp = xg + (4 * blk + hf) * (4 * MR * 16);
-                            const vkf_h8 xl = *(const vkf_h8 *)xp;
-                            const vkf_h8 xh = *(const vkf_h8 *)(xp + 2 * (4 * MR * 16));
-                            const vkf_h8 bl = gm_decode_w<F, 0>(d0, d1, d, m, c64);
-                            const vkf_h8 bh = gm_decode_w<F, 1>(d0, d1, d, m, c64);
-                            y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bl, y4, 0, 0, 0);
-                            y4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bh, y4, 0, 0, 0);
-                        }
-                    }
-                }
+                    return xm;
+                };
+                gm_group<F>(tt[u], X, XM, lg, sel, c64, y4);
             }
         };
         if constexpr (gm_pingpong<F>()) {
@@ -804,3 +820,139 @@ VKF_GEMV_MFMA(q6_k, GF_Q6_K)
 VKF_GEMV_MFMA(q5_k, GF_Q5_K)
 VKF_GEMV_MFMA(q8_0, GF_Q8_0)
 VKF_GEMV_MFMA(q5_0, GF_Q5_0)
+
+// ---------------------------------------------------------------------------
+// fp16 activations in registers (gemv_mfma_xr).  The P waves of a
+// workgroup split K P ways: wave w owns the 256-k groups [w*G/P,
+// (w+1)*G/P) (at most NG of them) of every tile and holds those groups'
+// activation pieces in registers for the whole launch, in the decode's k
+// order (no LDS image, no staging barrier; Q4_K / Q5_K also hold the
+// sub-block sums of x for the min-term MFMA, added across the lane pair
+// that shares each sub-block).  The workgroup walks its tiles one per
+// round: a wave multiplies its groups of the round's tile, requests the
+// next round's weights, and the P partial tiles meet in LDS, where wave 0
+// adds them in wave order.  Rows >= M of the MFMA operand repeat row M - 1
+// (MR = M rounded up to 4, 8 or 16) and feed discarded outputs.
+// ---------------------------------------------------------------------------
+template <int F, uint32_t MR, int NG, int P>
+__device__ __forceinline__ void gemv_mfma_xr(const VkfGemvArgs &a, unsigned char *smem) {
+    const uint32_t nsb = a.K / 256;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int li = lane & 15, lg = lane >> 4;
+    const uint32_t ntiles = (a.N + 15) / 16;
+    // this wave's groups [g0, g0 + ng), ng <= NG (the host's choice of P)
+    const uint32_t g0 = wave * nsb / P, ng = (wave + 1) * nsb / P - g0;
+    const uint32_t arow = li < (int)MR ? li : li & (MR - 1);
+    const uint32_t xrow = arow < a.M ? arow : a.M - 1;
+    const _Float16 *xp = (const _Float16 *)a.x + (uint64_t)xrow * a.ldx;
+    vkf_h8 xr[NG][8];
+#pragma unroll
+    for (int u = 0; u < NG; u++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const uint32_t g = g0 + (u < (int)ng ? u : 0);
+            const vkf_u4 v = *(const vkf_u4 *)(xp + 256 * g + gm_k0<F>(t, lg));
+            xr[u][t] = __builtin_bit_cast(vkf_h8, gm_reorder(v));
+        }
+    // Q4_K / Q5_K: lane (i, g) holds half of each of the sub-blocks
+    // J = {2h, 2h+1, 4+2h, 5+2h}, h = g >> 1 (steps t = 4(j>>2) + 2(j&1)
+    // and t + 1); the other half is in lane (i, g ^ 1).  Even k-slices
+    // carry xs/32 of J as 4 fp16 hi parts, then 4 lo parts (order
+    // (j & 1) + 2(j >> 2)); odd ones zero.
+    vkf_h8 xmr[gm_kmin<F>() ? NG : 1];
+    if constexpr (gm_kmin<F>()) {
+        const vkf_h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+        for (int u = 0; u < NG; u++) {
+            vkf_h8 m = {};
+#pragma unroll
+            for (int pos = 0; pos < 4; pos++) {
+                const int t0 = 4 * (pos >> 1) + 2 * (pos & 1);
+                float f = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const vkf_u4 v = __builtin_bit_cast(vkf_u4, xr[u][t0 + q]);
+#pragma unroll
+                    for (int d = 0; d < 4; d++) {
+                        const uint32_t w = v[d];
+                        f = __builtin_amdgcn_fdot2(__builtin_bit_cast(vkf_h2, w), ones, f, false);
+                    }
+                }
+                f += __shfl_xor(f, 16, 64);
+                const float fs = f * 0.03125f;
+                const _Float16 hi = (_Float16)fs, lo = (_Float16)(fs - (float)hi);
+                m[pos] = hi;
+                m[4 + pos] = lo;
+            }
+            xmr[u] = (lg & 1) == 0 ? m : vkf_h8{};
+        }
+    }
+    const uint32_t sel = (lg >> 1) ? 0x04030402u : 0x04010400u;  // bytes 2h, 2h+1 as (1024 + v) fp16
+    GmSb<F> ta[NG];
+    auto load_round = [&](uint32_t tile, GmSb<F> *t) {
+        const uint32_t n = tile * 16 + li;
+        const uint8_t *row = a.w + (uint64_t)(n < a.N ? n : a.N - 1) * a.row_bytes;
+#pragma unroll
+        for (int u = 0; u < NG; u++) gm_load<F>(row, g0 + (u < (int)ng ? u : 0), lg, t[u]);
+    };
+    uint32_t c64 = 0x64006400u;
+    asm volatile("" : "+v"(c64));
+    float *red = (float *)smem;  // [P waves][64 lanes][4]
+    const vkf_f4 zero = {0, 0, 0, 0};
+    auto round = [&](uint32_t tile, GmSb<F> *cur) {
+        vkf_f4 y4 = zero;
+#pragma unroll
+        for (int u = 0; u < NG; u++) {
+            if (u < (int)ng) {
+                const auto X = [&](int t) { return xr[u][t]; };
+                const auto XM = [&]() {
+                    if constexpr (gm_kmin<F>()) return xmr[u];
+                    else return vkf_h8{};
+                };
+                gm_group<F>(cur[u], X, XM, lg, sel, c64, y4);
+            }
+        }
+        // the next round's weights load under the reduction
+        if (tile + gridDim.x < ntiles && ng > 0) load_round(tile + gridDim.x, cur);
+        *(vkf_f4 *)(red + (wave * 64 + lane) * 4) = y4;
+        __syncthreads();
+        if (wave == 0) {
+            vkf_f4 s = y4;
+            for (int w = 1; w < P; w++) {
+                const vkf_f4 v = *(const vkf_f4 *)(red + (w * 64 + lane) * 4);
+#pragma unroll
+                for (int e = 0; e < 4; e++) s[e] += v[e];
+            }
+            const uint32_t n = tile * 16 + li;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t m = 4 * lg + e;
+                if (m < a.M && n < a.N) {
+                    float *yp = a.y + (uint64_t)m * a.ldy + n;
+                    *yp = (a.flags & 1u) ? *yp + s[e] : s[e];
+                }
+            }
+        }
+        __syncthreads();
+    };
+    uint32_t tile = blockIdx.x;
+    if (tile < ntiles && ng > 0) load_round(tile, ta);
+    for (; tile < ntiles; tile += gridDim.x) round(tile, ta);  // workgroup-uniform
+}
+
+template <int F, int NG, int P>
+__device__ __forceinline__ void gemv_mfma_xr_entry(const VkfGemvArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    if (a.M <= 4) gemv_mfma_xr<F, 4, NG, P>(a, smem);
+    else if (a.M <= 8) gemv_mfma_xr<F, 8, NG, P>(a, smem);
+    else gemv_mfma_xr<F, 16, NG, P>(a, smem);
+}
+// vkf_gemv_mfma_xr_<q>_f16_p<P>: P waves, up to NG = ceil(G / P) groups each
+#define VKF_GEMV_MFMA_XR(name, F, NG, P)                                                                   \
+    VKF_KERNEL void __launch_bounds__(64 * P) vkf_gemv_mfma_xr_##name##_f16_p##P(VkfGemvArgs a) {        \
+        gemv_mfma_xr_entry<F, NG, P>(a);                                                                 \
+    }
+VKF_GEMV_MFMA_XR(q4_0, GF_Q4_0, 1, 16)
+VKF_GEMV_MFMA_XR(q4_1, GF_Q4_1, 1, 16)
+VKF_GEMV_MFMA_XR(q4_k, GF_Q4_K, 2, 10)
