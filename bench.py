@@ -245,7 +245,9 @@ def run_suite(torch, ops, O, replays, only=None):
         rng = np.random.default_rng(_seed(6, M + N + K + tb))
         a = torch.from_numpy(rng.normal(0, 1, (M, K)).astype(np.float16)).to(dev)
         b = torch.from_numpy(rng.normal(0, 1, (N, K) if tb else (K, N)).astype(np.float16)).to(dev)
-        copies = _rotating_copies(torch, b, b.numel() * 2)
+        # at most 64 copies: a B of a few MB stays in the 256 MB MALL whatever
+        # the rotation, so small shapes gain nothing from thousands of copies
+        copies = _rotating_copies(torch, b, max(b.numel() * 2, ROTATE_BYTES // 64))
         d = torch.empty((M, N), dtype=torch.float16, device=dev)
         nl = max(32, len(copies))
         fl = 2.0 * M * N * K
