@@ -181,6 +181,57 @@ def test_linear_dense_split_k_and_plain(dev):
         assert rel_err(D.cpu().numpy(), ref) <= TOL_F32, (M, N, K)
 
 
+def _narrow_nb(M, N, K, es, cus, batch=1):
+    """The tile width the host picks for the narrow-tile kernels (16*nb
+    columns), 0 if it takes another kernel (mirrors narrow_nb in
+    csrc/host/vkf_runtime.cpp)."""
+    rows = -(-M // 128) * batch
+    if K == 0 or (K * es) % 256 or rows * -(-N // 128) >= cus:
+        return 0
+    for nb in (4, 5):
+        if rows * -(-N // (16 * nb)) <= cus:
+            return nb
+    return 0
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 5120, 5120), (512, 4096, 1024), (500, 5000, 768), (128, 8192, 2048),
+                                   (77, 200, 256), (384, 3000, 512)])
+def test_linear_dense_narrow_tiles(dev, M, N, K):
+    """Grids of fewer 128x128 tiles than CUs with whole pairs of K steps:
+    the narrow-tile kernels (128 x 64 or 128 x 80 tiles, three stages, K
+    split between two wave groups).  int8 -> exact int32 (also with integer
+    alpha / beta), fp16 -> fp32 and fp16 with alpha, beta*C, bias-free
+    activation; repeated calls give the same bits."""
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_FP16, DTYPE_FP16_FP32OUT, DTYPE_INT8_INT32OUT
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert _narrow_nb(M, N, K, 1, cus) in (4, 5) and _narrow_nb(M, N, K, 2, cus) in (4, 5)
+    rng = np.random.default_rng(seed_for(4, 82) + M + N + K)
+    A = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    Ci = rng.integers(-1000, 1000, (M, N)).astype(np.int32)
+    ref = A.astype(np.int64) @ W.astype(np.int64).T
+    D = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8_INT32OUT, transB=1)
+    D2 = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8_INT32OUT, transB=1,
+                    C=to_dev(Ci, dev), alpha=3, beta=-2)
+    torch.cuda.synchronize()
+    got = D.cpu().numpy().astype(np.int64)
+    assert np.array_equal(got, ref), (M, N, K, int((got != ref).sum()))
+    want2 = (3 * ref - 2 * Ci.astype(np.int64)).astype(np.int32)  # int32 wrap-around, as the kernel
+    assert np.array_equal(D2.cpu().numpy(), want2)
+    Af, Bf, C = _f16(rng, M, K), _f16(rng, N, K), _f16(rng, M, N)
+    reff = Af.astype(np.float64) @ Bf.astype(np.float64).T
+    outs = [ops.linear(to_dev(Af, dev), to_dev(Bf, dev), M, N, K, DTYPE_FP16_FP32OUT, transB=1) for _ in range(2)]
+    E = ops.linear(to_dev(Af, dev), to_dev(Bf, dev), M, N, K, DTYPE_FP16, transB=1, act=2,
+                   C=to_dev(C, dev), alpha=0.5, beta=0.25)
+    torch.cuda.synchronize()
+    assert rel_err(outs[0].cpu().numpy(), reff) <= TOL_F32, (M, N, K)
+    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+    pre = (0.5 * reff + 0.25 * C.astype(np.float64)).astype(np.float32)
+    assert rel_err(E.cpu().numpy().astype(np.float32), O.np_act(2, pre)) <= TOL_F16
+
+
 def test_linear_dense_split_k_repeatable(dev):
     """The split-K kernel adds the two groups' fp32 sums in one fixed order:
     the same inputs give the same bits on every call."""

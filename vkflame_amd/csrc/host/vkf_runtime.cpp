@@ -181,6 +181,21 @@ static bool skinny_ok(const VkfGemmArgs &g, uint32_t batch) {
     return !(g.flags & VKF_GF_Y_TRANS) || g.Cn % 8 == 0;
 }
 
+// The narrow-tile kernels (vkf_gemm_{f16,i8}_n{4,5}, kernels/gemm.hip):
+// 128 x 16·nb tiles, three stages of both K groups' steps, whole pairs of
+// 128-byte K steps.  The narrowest tile whose grid fits one tile per CU
+// (the least traffic per CU with the most CUs busy); 0 when neither fits
+// or the 128 x 128 grid already fills the CUs.
+constexpr uint32_t kNarrowStages = 3;
+static uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es) {
+    if (g.K == 0 || ((uint64_t)g.K * es) % 256 != 0) return 0;
+    const uint64_t cus = (uint64_t)cu_count(), rows = ((uint64_t)g.R + 127) / 128 * batch;
+    if (rows * (((uint64_t)g.Cn + 127) / 128) >= cus) return 0;
+    for (uint32_t nb = 4; nb <= 5; nb++)
+        if (rows * (((uint64_t)g.Cn + 16 * nb - 1) / (16 * nb)) <= cus) return nb;
+    return 0;
+}
+
 hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream, uint32_t batch) {
     if (g.R == 0 || g.Cn == 0 || batch == 0) return hipSuccess;
     dim3 grid((g.Cn + 127) / 128, (g.R + 127) / 128, batch);
@@ -196,9 +211,20 @@ hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream,
         (batch == 1 || ((g.bsx | g.bsy) & 15) == 0)) {
         const uint32_t es = id == VKF_K_GEMM_F16 ? 2 : 1;
         if (dma_operand(g.X, g.ldx, (g.flags & VKF_GF_X_TRANS) != 0, g.K, es) &&
-            dma_operand(g.Y, g.ldy, (g.flags & VKF_GF_Y_TRANS) != 0, g.K, es))
+            dma_operand(g.Y, g.ldy, (g.flags & VKF_GF_Y_TRANS) != 0, g.K, es)) {
+            // narrow tiles (128 x 16·nb) where they give the CUs more of the
+            // grid: the widest whose grid still fits one tile per CU
+            const uint32_t nb = narrow_nb(g, batch, es);
+            if (nb) {
+                static const VkfKernelId nk[2][2] = {{VKF_K_GEMM_I8_N4, VKF_K_GEMM_I8_N5},
+                                                     {VKF_K_GEMM_F16_N4, VKF_K_GEMM_F16_N5}};
+                const dim3 gn((g.Cn + 16 * nb - 1) / (16 * nb), grid.y, batch);
+                return launch(nk[es - 1][nb - 4], gn, dim3(512), &g, sizeof(g), stream,
+                              kNarrowStages * 2 * (16384 + nb * 16 * 128));
+            }
             return launch(id == VKF_K_GEMM_F16 ? VKF_K_GEMM_F16_K2 : VKF_K_GEMM_I8_K2, grid, dim3(512), &g,
                           sizeof(g), stream);
+        }
     }
     return launch(id, grid, dim3(256), &g, sizeof(g), stream);
 }

@@ -118,6 +118,10 @@
     X(GEMM_I8, "vkf_gemm_i8")                               \
     X(GEMM_F16_K2, "vkf_gemm_f16_k2")                       \
     X(GEMM_I8_K2, "vkf_gemm_i8_k2")                         \
+    X(GEMM_F16_N4, "vkf_gemm_f16_n4")                       \
+    X(GEMM_F16_N5, "vkf_gemm_f16_n5")                       \
+    X(GEMM_I8_N4, "vkf_gemm_i8_n4")                         \
+    X(GEMM_I8_N5, "vkf_gemm_i8_n5")                         \
     X(GEMV_MFMA_XR_Q4_0_F16, "vkf_gemv_mfma_xr_q4_0_f16_p16") \
     X(GEMV_MFMA_XR_Q4_1_F16, "vkf_gemv_mfma_xr_q4_1_f16_p16") \
     X(GEMV_MFMA_XR_Q4_K_F16_P10, "vkf_gemv_mfma_xr_q4_k_f16_p10") \

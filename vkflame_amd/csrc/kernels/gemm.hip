@@ -408,7 +408,7 @@ __device__ __forceinline__ void wait_vm() {
     if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
     else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else static_assert(N == 0, "wait_vm: unsupported count");
+    else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 __device__ __forceinline__ bool dma_ok(const void *P, uint64_t ld, bool trans, uint32_t K, int ES) {
@@ -2189,3 +2189,234 @@ VKF_KERNEL void __launch_bounds__(64 * SK_WAVES) vkf_gemm_f16_skinny(VkfGemmArgs
         else gemm_skinny<4, false>(a, sk_smem);
     }
 }
+
+// ---------------------------------------------------------------------------
+// Dense GEMM on narrow tiles for grids of fewer 128 x 128 tiles than CUs:
+// 128 x 16·NB tiles (NB = 4 or 5: 64 or 80 columns), NB picked on the host
+// as the widest tile whose grid still fits one tile per CU (M = 512,
+// N = 5120: 4 x 64 = 256 tiles of 128 x 80, where 128 x 128 tiles give 160
+// and leave 96 CUs idle).  At these sizes a CU's time is its tile traffic
+// over the rate one CU can pull from L2 / MALL, which is set by the bytes it
+// keeps in flight; the narrower tile moves (128 + 16·NB)·K instead of 256·K
+// elements per CU, on every CU, and leaves room for three stages.
+// K is split inside the workgroup as in the split-K kernels: waves 0-3 take
+// the even 128-byte K steps and waves 4-7 the odd ones; wave q of a group
+// owns rows 32q .. 32q + 31 of the tile and all its columns (2 x NB
+// fragments of 16 x 16).  Three stages of both groups' steps (3 x 52 KiB
+// for NB = 5) keep two pairs of steps in flight while one is multiplied.
+// The group sums meet in LDS in a fixed order (int32 exact, fp32
+// repeatable).  Conditions (host): X and Y K-contiguous, 16-byte aligned,
+// 16-byte rows, K·ES % 256 == 0 (whole pairs of steps).
+// ---------------------------------------------------------------------------
+template <int NB>
+constexpr uint32_t gn_pair_bytes() { return 2 * (16384 + NB * 16 * 128); }
+#define GN_STAGES 3
+
+template <int ES, int NB, class ACC>
+__device__ __forceinline__ void mfma_step_n(const uint8_t *lx, const uint8_t *ly, int wq, ACC acc[2][NB]) {
+    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4, sw = li & 7;
+    vkf_i4 fa[2][2], fb[2][NB];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int c = 4 * s + lg;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            fa[s][i] = *(const vkf_i4 *)(lx + (wq * 32 + 16 * i + li) * 128 + ((c ^ sw) << 4));
+#pragma unroll
+        for (int j = 0; j < NB; j++) fb[s][j] = *(const vkf_i4 *)(ly + (16 * j + li) * 128 + ((c ^ sw) << 4));
+    }
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) acc[i][j] = mfma_frag<ES>(fa[s][i], fb[s][j], acc[i][j]);
+    __builtin_amdgcn_s_setprio(0);
+}
+
+template <int ES, int NB, class ACC>
+__device__ __forceinline__ void gemm_mainloop_n(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, ACC acc[2][NB],
+                                                uint8_t *smem) {
+    constexpr uint32_t SX = 16384, SG = SX + NB * 16 * 128, SP = 2 * SG;
+    constexpr int NCH = 2 * NB;             // 8-row chunks of the Y tile
+    constexpr int NYC = (NCH + 3) / 4;      // the most chunks one wave loads
+    const int wave = threadIdx.x >> 6, g = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
+    const int ny = (NCH - wq + 3) / 4;      // this wave's chunks: wq, wq + 4, ...
+    const uint32_t npair = (uint32_t)(((uint64_t)a.K * ES) / 256);
+    const uint8_t *gx[4], *gy[NYC];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t rr = (4 * wq + j) * 8 + (lane >> 3);
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t rx = r0 + rr < a.R ? r0 + rr : a.R - 1;  // rows past the edge: any valid row
+        gx[j] = (const uint8_t *)a.X + (uint64_t)rx * a.ldx * ES + ch * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < NYC; j++) {
+        const uint32_t rr = (wq + 4 * j) * 8 + (lane >> 3);
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t ry = c0 + rr < a.Cn ? c0 + rr : a.Cn - 1;
+        gy[j] = (const uint8_t *)a.Y + (uint64_t)ry * a.ldy * ES + ch * 16;
+    }
+    // this group's step of pair p into stage st
+    auto issue = [&](uint32_t p, uint32_t st) {
+        const uint64_t ko = (uint64_t)(2 * p + g) * 128;
+        uint8_t *sx = smem + st * SP + g * SG, *sy = sx + SX;
+#pragma unroll
+        for (int j = 0; j < 4; j++) vkf_load_lds16(gx[j] + ko, sx + (4 * wq + j) * 1024);
+#pragma unroll
+        for (int j = 0; j < NYC; j++)
+            if (j < ny) vkf_load_lds16(gy[j] + ko, sy + (wq + 4 * j) * 1024);
+    };
+    if (npair > 0) issue(0, 0);
+    if (npair > 1) issue(1, 1);
+    uint32_t st = 0;  // stage of pair t
+    for (uint32_t t = 0; t < npair; t++) {
+        // pair t landed; pair t + 1 (4 + ny loads of this wave) may stay in flight
+        if (t + 1 < npair) {
+            if (ny == NYC) wait_vm<4 + NYC>();
+            else wait_vm<4 + NYC - 1>();
+        } else {
+            wait_vm<0>();
+        }
+        __syncthreads();  // every wave's part of pair t is in LDS; pair t - 1's stage is free
+        if (t + 2 < npair) issue(t + 2, st == 0 ? 2 : st - 1);
+        const uint8_t *lx = smem + st * SP + g * SG;
+        mfma_step_n<ES, NB>(lx, lx + SX, wq, acc);
+        st = st == 2 ? 0 : st + 1;
+    }
+    __syncthreads();  // LDS free for the group sum
+    // group 1's accumulators to LDS, group 0 adds them
+    vkf_i4 *red = (vkf_i4 *)smem;
+    if (g == 1) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) red[(wq * 2 * NB + i * NB + j) * 64 + lane] = __builtin_bit_cast(vkf_i4, acc[i][j]);
+    }
+    __syncthreads();
+    if (g == 0) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) acc[i][j] += __builtin_bit_cast(ACC, red[(wq * 2 * NB + i * NB + j) * 64 + lane]);
+    }
+    __syncthreads();  // LDS free for the epilogue
+}
+
+// Workgroup -> 128 x CT tile, XCD-aware as gemm_tile_of: column tiles dealt
+// to the 8 XCDs round-robin, each XCD running all row tiles of a column.
+template <uint32_t CT>
+__device__ __forceinline__ void gemm_tile_of_n(uint32_t &r0, uint32_t &c0) {
+    const uint32_t nc = gridDim.x, nr = gridDim.y, id = blockIdx.x + nc * blockIdx.y;
+    const uint32_t full = nc & ~7u;
+    uint32_t r, c;
+    if (id < full * nr) {
+        const uint32_t x = id & 7u, sl = id >> 3;
+        c = (sl / nr) * 8 + x;
+        r = sl % nr;
+    } else {
+        const uint32_t j = id - full * nr;
+        c = full + j / nr;
+        r = j % nr;
+    }
+    r0 = r * 128;
+    c0 = c * CT;
+}
+
+// The float epilogue (epi_one per value) of group 0's sums through an fp32
+// tile in LDS, then 16-byte row stores by all 512 threads.  D_I32: group 0
+// stores the raw int32 sums with integer alpha / beta.
+template <int ES, int NB, class ACC>
+__device__ __forceinline__ void gemm_epilogue_n(const VkfGemmArgs &a, uint32_t r0, uint32_t c0,
+                                                const ACC acc[2][NB], uint8_t *smem) {
+    constexpr uint32_t CT = 16 * NB, TP = CT + 4;
+    const int wave = threadIdx.x >> 6, wq = wave & 3, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+    if constexpr (ES == 1) {
+        if (a.flags & VKF_GF_D_I32) {
+            if (wave >= 4) return;  // group 0 holds the sums; no barrier follows
+            const int32_t al = __builtin_bit_cast(int32_t, a.alpha), be = __builtin_bit_cast(int32_t, a.beta);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < NB; j++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint32_t r = r0 + wq * 32 + 16 * i + 4 * lg + e, c = c0 + 16 * j + li;
+                        if (r < a.R && c < a.Cn) {
+                            int32_t v = acc[i][j][e];
+                            if (al != 1 || be != 0)
+                                v = al * v + (be ? be * ((const int32_t *)a.Cin)[(uint64_t)r * a.ldc + c] : 0);
+                            ((int32_t *)a.D)[(uint64_t)r * a.ldd + c] = v;
+                        }
+                    }
+            return;
+        }
+    }
+    float *tile = (float *)smem;
+    if (wave < 4) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t tr = wq * 32 + 16 * i + 4 * lg + e, r = r0 + tr < a.R ? r0 + tr : a.R - 1;
+#pragma unroll
+                for (int j = 0; j < NB; j++) {
+                    const uint32_t tc = 16 * j + li, c = c0 + tc < a.Cn ? c0 + tc : a.Cn - 1;
+                    tile[tr * TP + tc] = epi_one(a, r, c, (float)acc[i][j][e]);
+                }
+            }
+    }
+    __syncthreads();
+    const bool f32 = (a.flags & VKF_GF_D_F32) != 0;
+    const uint32_t vec = f32 ? 4 : 8;  // elements per 16-byte store
+    const bool vok = (a.ldd % vec) == 0 && (((uintptr_t)a.D & 15) == 0);
+    const uint32_t per_row = CT / vec;
+    for (uint32_t q = threadIdx.x; q < 128 * per_row; q += 512) {
+        const uint32_t tr = q / per_row, tc = (q % per_row) * vec;
+        const uint32_t r = r0 + tr, c = c0 + tc;
+        if (r >= a.R || c >= a.Cn) continue;
+        const float *src = tile + tr * TP + tc;
+        if (vok && c + vec <= a.Cn) {
+            if (f32) {
+                *(vkf_f4 *)((float *)a.D + (uint64_t)r * a.ldd + c) = *(const vkf_f4 *)src;
+            } else {
+                vkf_h8 h;
+#pragma unroll
+                for (int k = 0; k < 8; k++) h[k] = vkf_to_f16(src[k]);
+                *(vkf_h8 *)((_Float16 *)a.D + (uint64_t)r * a.ldd + c) = h;
+            }
+        } else {
+            for (uint32_t k = 0; k < vec && c + k < a.Cn; k++) {
+                if (f32) ((float *)a.D)[(uint64_t)r * a.ldd + c + k] = src[k];
+                else ((_Float16 *)a.D)[(uint64_t)r * a.ldd + c + k] = vkf_to_f16(src[k]);
+            }
+        }
+    }
+}
+
+template <int ES, int NB, class ACC>
+__device__ __forceinline__ void gemm_n_body(const VkfGemmArgs &a0, uint8_t *smem) {
+    const VkfGemmArgs a = gemm_batch(a0);
+    uint32_t r0, c0;
+    gemm_tile_of_n<16 * NB>(r0, c0);
+    ACC acc[2][NB];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] = ACC{0, 0, 0, 0};
+    gemm_mainloop_n<ES, NB>(a, r0, c0, acc, smem);
+    gemm_epilogue_n<ES, NB>(a, r0, c0, acc, smem);
+}
+
+// dynamic LDS: GN_STAGES x gn_pair_bytes<NB>() (156 KiB for NB = 5)
+#define VKF_GEMM_N(name, ES, ACC, NB)                                                \
+    VKF_KERNEL void __launch_bounds__(512) vkf_gemm_##name##_n##NB(VkfGemmArgs a) { \
+        extern __shared__ __attribute__((aligned(16))) uint8_t gn_smem[];          \
+        gemm_n_body<ES, NB, ACC>(a, gn_smem);                                        \
+    }
+VKF_GEMM_N(f16, 2, vkf_f4, 4)
+VKF_GEMM_N(f16, 2, vkf_f4, 5)
+VKF_GEMM_N(i8, 1, vkf_i4, 4)
+VKF_GEMM_N(i8, 1, vkf_i4, 5)
