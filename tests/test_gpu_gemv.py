@@ -276,6 +276,24 @@ def test_gemv_mfma(dev, qt, M, N, K):
     assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32
 
 
+@pytest.mark.parametrize("qt,K", [(O.Q4_0, 2304), (O.Q4_0, 4096), (O.Q4_1, 4096), (O.Q4_K, 2304), (O.Q4_K, 5120)],
+                         ids=["q4_0-2304", "q4_0-4096", "q4_1-4096", "q4_k-2304", "q4_k-5120"])
+@pytest.mark.parametrize("M", [3, 16])
+def test_gemv_mfma_many_rounds(dev, qt, K, M):
+    """The register-activation kernel on more 16-row tiles than two rounds of
+    one workgroup per CU (the weights of the round after next staged in LDS
+    while a round computes) with a ragged last tile; K = 2304 leaves some
+    waves without groups."""
+    import torch
+    from vkflame_amd import ops
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    N = 16 * cus * 2 + 40
+    w = O.gen_weight(qt, N, K, seed_for(2, 90 + M + 20 * qt))
+    xa, x64 = _x("f16", M, K, seed_for(2, 95 + M))
+    y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
+    assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32
+
+
 @pytest.mark.parametrize("M", [2, 5, 8, 9, 16])
 @pytest.mark.parametrize("N", [77, 3001])
 @pytest.mark.parametrize("K", [2560, 13824])
