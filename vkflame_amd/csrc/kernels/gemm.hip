@@ -2204,8 +2204,9 @@ VKF_KERNEL void __launch_bounds__(64 * SK_WAVES) vkf_gemm_f16_skinny(VkfGemmArgs
 // owns rows 32q .. 32q + 31 of the tile and all its columns (2 x NB
 // fragments of 16 x 16).  Three stages of both groups' steps (3 x 52 KiB
 // for NB = 5) keep two pairs of steps in flight while one is multiplied.
-// The group sums meet in LDS in a fixed order (int32 exact, fp32
-// repeatable).  Conditions (host): X and Y K-contiguous, 16-byte aligned,
+// The group partials meet in LDS, each group then finishing half the tile
+// (int32 exact; fp32 the same bits as one group adding both).  Conditions
+// (host): X and Y K-contiguous, 16-byte aligned,
 // 16-byte rows, K·ES % 256 == 0 (whole pairs of steps).
 // ---------------------------------------------------------------------------
 template <int NB>
@@ -2286,22 +2287,35 @@ __device__ __forceinline__ void gemm_mainloop_n(const VkfGemmArgs &a, uint32_t r
         mfma_step_n<ES, NB>(lx, lx + SX, wq, acc);
         st = st == 2 ? 0 : st + 1;
     }
-    __syncthreads();  // LDS free for the group sum
-    // group 1's accumulators to LDS, group 0 adds them
-    vkf_i4 *red = (vkf_i4 *)smem;
-    if (g == 1) {
+    __syncthreads();  // LDS free for the group sums
+}
+
+// The two groups' partial tiles meet in LDS: group g keeps its 16-row
+// fragment row i = g (rows 32q + 16g .. + 15 of wave q's 32), sends the
+// other to LDS and adds the other group's partial of its own, so each group
+// then holds the sums of half the tile (fp32: a + b == b + a, the same bits
+// whichever group adds).
+template <int NB, class ACC>
+__device__ __forceinline__ void gemm_group_exchange_n(ACC acc[2][NB], ACC mine[NB], uint8_t *smem) {
+    const int wave = threadIdx.x >> 6, g = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
+    vkf_i4 *red = (vkf_i4 *)smem;  // [group that sends][wave][NB][64 lanes]
+    const bool g1 = g != 0;
+    // element-wise selects (no indexing of acc by g, which would put it in scratch)
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+    for (int j = 0; j < NB; j++) {
+        const vkf_i4 a0 = __builtin_bit_cast(vkf_i4, acc[0][j]), a1 = __builtin_bit_cast(vkf_i4, acc[1][j]);
+        vkf_i4 snd, keep;
 #pragma unroll
-            for (int j = 0; j < NB; j++) red[(wq * 2 * NB + i * NB + j) * 64 + lane] = __builtin_bit_cast(vkf_i4, acc[i][j]);
+        for (int e = 0; e < 4; e++) {
+            snd[e] = g1 ? a0[e] : a1[e];
+            keep[e] = g1 ? a1[e] : a0[e];
+        }
+        red[((g * 4 + wq) * NB + j) * 64 + lane] = snd;
+        mine[j] = __builtin_bit_cast(ACC, keep);
     }
     __syncthreads();
-    if (g == 0) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int j = 0; j < NB; j++) acc[i][j] += __builtin_bit_cast(ACC, red[(wq * 2 * NB + i * NB + j) * 64 + lane]);
-    }
+    for (int j = 0; j < NB; j++) mine[j] += __builtin_bit_cast(ACC, red[(((g ^ 1) * 4 + wq) * NB + j) * 64 + lane]);
     __syncthreads();  // LDS free for the epilogue
 }
 
@@ -2325,48 +2339,82 @@ __device__ __forceinline__ void gemm_tile_of_n(uint32_t &r0, uint32_t &c0) {
     c0 = c * CT;
 }
 
-// The float epilogue (epi_one per value) of group 0's sums through an fp32
-// tile in LDS, then 16-byte row stores by all 512 threads.  D_I32: group 0
-// stores the raw int32 sums with integer alpha / beta.
+// A thread's row and column factors of the epilogue (row scale, column
+// scale, bias) for the 4 rows x NB columns it finishes, loaded before the
+// main loop so that their latency is hidden.
+template <int NB>
+struct EpiPreN {
+    float rs[4], br[4], cs[NB], bc[NB];
+};
+template <int NB>
+__device__ __forceinline__ EpiPreN<NB> epi_prefetch_n(const VkfGemmArgs &a, uint32_t r0, uint32_t c0) {
+    const int wave = threadIdx.x >> 6, g = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63, li = lane & 15,
+              lg = lane >> 4;
+    const bool bf32 = (a.flags & VKF_GF_BIAS_F32) != 0, brow = (a.flags & VKF_GF_BIAS_ROW) != 0;
+    EpiPreN<NB> p;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t tr = wq * 32 + 16 * g + 4 * lg + e, r = r0 + tr < a.R ? r0 + tr : a.R - 1;
+        p.rs[e] = a.rs ? a.rs[(a.flags & VKF_GF_RS_SCALAR) ? 0 : r] : 1.0f;
+        p.br[e] = (a.bias && brow) ? (bf32 ? ((const float *)a.bias)[r] : (float)((const _Float16 *)a.bias)[r]) : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const uint32_t tc = 16 * j + li, c = c0 + tc < a.Cn ? c0 + tc : a.Cn - 1;
+        p.cs[j] = a.cs ? a.cs[(a.flags & VKF_GF_CS_SCALAR) ? 0 : c] : 1.0f;
+        p.bc[j] = (a.bias && !brow) ? (bf32 ? ((const float *)a.bias)[c] : (float)((const _Float16 *)a.bias)[c]) : 0.0f;
+    }
+    return p;
+}
+
+// The float epilogue (epi_one's steps per value) of each group's half of
+// the sums through an fp32 tile in LDS, then 16-byte row stores by all 512
+// threads.  D_I32: each group stores its raw int32 sums with integer
+// alpha / beta.
 template <int ES, int NB, class ACC>
-__device__ __forceinline__ void gemm_epilogue_n(const VkfGemmArgs &a, uint32_t r0, uint32_t c0,
-                                                const ACC acc[2][NB], uint8_t *smem) {
+__device__ __forceinline__ void gemm_epilogue_n(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, const ACC mine[NB],
+                                                uint8_t *smem, const EpiPreN<NB> &pre) {
     constexpr uint32_t CT = 16 * NB, TP = CT + 4;
-    const int wave = threadIdx.x >> 6, wq = wave & 3, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+    const int wave = threadIdx.x >> 6, g = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63, li = lane & 15,
+              lg = lane >> 4;
     if constexpr (ES == 1) {
         if (a.flags & VKF_GF_D_I32) {
-            if (wave >= 4) return;  // group 0 holds the sums; no barrier follows
             const int32_t al = __builtin_bit_cast(int32_t, a.alpha), be = __builtin_bit_cast(int32_t, a.beta);
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int j = 0; j < NB; j++)
 #pragma unroll
-                for (int j = 0; j < NB; j++)
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const uint32_t r = r0 + wq * 32 + 16 * i + 4 * lg + e, c = c0 + 16 * j + li;
-                        if (r < a.R && c < a.Cn) {
-                            int32_t v = acc[i][j][e];
-                            if (al != 1 || be != 0)
-                                v = al * v + (be ? be * ((const int32_t *)a.Cin)[(uint64_t)r * a.ldc + c] : 0);
-                            ((int32_t *)a.D)[(uint64_t)r * a.ldd + c] = v;
-                        }
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t r = r0 + wq * 32 + 16 * g + 4 * lg + e, c = c0 + 16 * j + li;
+                    if (r < a.R && c < a.Cn) {
+                        int32_t v = mine[j][e];
+                        if (al != 1 || be != 0)
+                            v = al * v + (be ? be * ((const int32_t *)a.Cin)[(uint64_t)r * a.ldc + c] : 0);
+                        ((int32_t *)a.D)[(uint64_t)r * a.ldd + c] = v;
                     }
-            return;
+                }
+            return;  // no barrier follows
         }
     }
     float *tile = (float *)smem;
-    if (wave < 4) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+    for (int e = 0; e < 4; e++) {
+        const uint32_t tr = wq * 32 + 16 * g + 4 * lg + e, r = r0 + tr < a.R ? r0 + tr : a.R - 1;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t tr = wq * 32 + 16 * i + 4 * lg + e, r = r0 + tr < a.R ? r0 + tr : a.R - 1;
-#pragma unroll
-                for (int j = 0; j < NB; j++) {
-                    const uint32_t tc = 16 * j + li, c = c0 + tc < a.Cn ? c0 + tc : a.Cn - 1;
-                    tile[tr * TP + tc] = epi_one(a, r, c, (float)acc[i][j][e]);
-                }
+        for (int j = 0; j < NB; j++) {
+            const uint32_t tc = 16 * j + li, c = c0 + tc < a.Cn ? c0 + tc : a.Cn - 1;
+            // epi_one's steps, with the row and column factors from registers
+            float v = (float)mine[j][e];
+            if (a.rs) v *= pre.rs[e];
+            if (a.cs) v *= pre.cs[j];
+            v *= a.alpha;
+            if (a.beta != 0.0f) {
+                const float cin = (a.flags & VKF_GF_CIN_F32) ? ((const float *)a.Cin)[(uint64_t)r * a.ldc + c]
+                                                             : (float)((const _Float16 *)a.Cin)[(uint64_t)r * a.ldc + c];
+                v = fmaf(a.beta, cin, v);
             }
+            if (a.bias) v += (a.flags & VKF_GF_BIAS_ROW) ? pre.br[e] : pre.bc[j];
+            tile[tr * TP + tc] = vkf_act(a.act, v);
+        }
     }
     __syncthreads();
     const bool f32 = (a.flags & VKF_GF_D_F32) != 0;
@@ -2406,8 +2454,12 @@ __device__ __forceinline__ void gemm_n_body(const VkfGemmArgs &a0, uint8_t *smem
     for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int j = 0; j < NB; j++) acc[i][j] = ACC{0, 0, 0, 0};
+    EpiPreN<NB> pre{};
+    if (!(ES == 1 && (a.flags & VKF_GF_D_I32))) pre = epi_prefetch_n<NB>(a, r0, c0);
     gemm_mainloop_n<ES, NB>(a, r0, c0, acc, smem);
-    gemm_epilogue_n<ES, NB>(a, r0, c0, acc, smem);
+    ACC mine[NB];
+    gemm_group_exchange_n<NB>(acc, mine, smem);
+    gemm_epilogue_n<ES, NB>(a, r0, c0, mine, smem, pre);
 }
 
 // dynamic LDS: GN_STAGES x gn_pair_bytes<NB>() (156 KiB for NB = 5)
