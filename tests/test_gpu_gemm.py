@@ -492,11 +492,35 @@ def test_wide_q6_k_q8_1_k5120(dev):
     assert rel_err(y.cpu().numpy(), O.ref_gemv(x64, O.np_dequant(O.Q6_K, w).reshape(N, K))) <= TOL_F32
 
 
+@pytest.mark.parametrize("M,N,K", [(512, 4096, 1024), (512, 5120, 2304), (300, 5000, 1280), (128, 8200, 512),
+                                   (17, 100, 256), (200, 77, 768)])
+def test_gemm_q4_k_narrow_tiles(dev, M, N, K):
+    """Q4_K x fp16 on 128-row grids of fewer tiles than CUs: the narrow-tile
+    kernel with raw Q4_K pieces staged three steps ahead (128 x 64 or
+    128 x 80 tiles, ragged rows and columns, K from one super-block), fp32
+    out against the oracle's float64 product; repeated calls give the same
+    bits."""
+    import torch
+    from vkflame_amd import ops
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert _narrow_nb(M, N, K, 2, cus) in (4, 5)
+    w = O.gen_weight(O.Q4_K, N, K, seed_for(3, 600 + M + N))
+    x = _f16(np.random.default_rng(seed_for(3, 700 + K)), M, K)
+    wd, xd = to_dev(w, dev), to_dev(x, dev)
+    y = ops.gemm_q(wd, O.Q4_K, xd, N, K)
+    y2 = ops.gemm_q(wd, O.Q4_K, xd, N, K)
+    torch.cuda.synchronize()
+    ref = O.ref_gemv(x.astype(np.float64), O.np_dequant(O.Q4_K, w).reshape(N, K))
+    assert rel_err(y.cpu().numpy(), ref) <= TOL_F32
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+
+
 def test_config3_q4_k_prefill_5120x13824(dev):
     """C3's second shape at M = 512: Q4_K 5120 x 13824 (the down projection),
-    fp16 activations.  40 x 4 = 160 tiles of 128 x 128 on a 256-CU MI355X:
-    the split-K kernel (vkf_gemm_q4_k_f16_k2), the route bench.py times.  All
-    512 activation rows against the oracle on 514 weight rows."""
+    fp16 activations.  40 x 4 = 160 tiles of 128 x 128 on a 256-CU MI355X,
+    so the narrow-tile kernel (vkf_gemm_q4_k_f16_n5, 256 tiles of 128 x 80),
+    the route bench.py times.  All 512 activation rows against the oracle on
+    514 weight rows."""
     import torch
     from vkflame_amd import ops
     N, K, M = 5120, 13824, 512

@@ -394,6 +394,19 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
                            S(stream));
     }
     dim3 grid(cdiv(N, 128), cdiv(M, 128));
+    // Q4_K on 128-row grids of fewer tiles than CUs: narrow tiles, with the
+    // raw weight blocks staged by direct-to-LDS loads like the activations
+    // (kernels/gemm.hip gemm_mainloop_q4k_n; LDS: X 96 KiB, fp16 weights
+    // nb·8 KiB, raw pieces nb·4.5 KiB)
+    if (qt == VKF_Q4_K && xk == 0 && aligned(x, 16) && (ldx % 8) == 0 && (K % 256) == 0 && aligned(w, 16) &&
+        (row_bytes % 16) == 0) {
+        const uint32_t nb = vkf::narrow_nb(g, 1, 2);
+        if (nb) {
+            const size_t lds = 98304 + (size_t)nb * (4 * 2048 + 6 * 768);
+            return vkf::launch(nb == 4 ? VKF_K_GEMM_Q4_K_F16_N4 : VKF_K_GEMM_Q4_K_F16_N5,
+                               dim3(cdiv(N, 16 * nb), cdiv(M, 128)), dim3(512), g, S(stream), lds);
+        }
+    }
     // 128-row grids of at most one tile per CU: the 512-thread kernel that
     // splits K between two wave groups (kernels/gemm.hip
     // gemm_mainloop_qdma_k2), same direct-to-LDS conditions as above

@@ -181,13 +181,13 @@ static bool skinny_ok(const VkfGemmArgs &g, uint32_t batch) {
     return !(g.flags & VKF_GF_Y_TRANS) || g.Cn % 8 == 0;
 }
 
-// The narrow-tile kernels (vkf_gemm_{f16,i8}_n{4,5}, kernels/gemm.hip):
+// The narrow-tile kernels (vkf_gemm_{f16,i8,q4_k_f16}_n{4,5}, kernels/gemm.hip):
 // 128 x 16·nb tiles, three stages of both K groups' steps, whole pairs of
 // 128-byte K steps.  The narrowest tile whose grid fits one tile per CU
 // (the least traffic per CU with the most CUs busy); 0 when neither fits
 // or the 128 x 128 grid already fills the CUs.
 constexpr uint32_t kNarrowStages = 3;
-static uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es) {
+uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es) {
     if (g.K == 0 || ((uint64_t)g.K * es) % 256 != 0) return 0;
     const uint64_t cus = (uint64_t)cu_count(), rows = ((uint64_t)g.R + 127) / 128 * batch;
     if (rows * (((uint64_t)g.Cn + 127) / 128) >= cus) return 0;

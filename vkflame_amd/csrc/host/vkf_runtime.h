@@ -122,6 +122,8 @@
     X(GEMM_F16_N5, "vkf_gemm_f16_n5")                       \
     X(GEMM_I8_N4, "vkf_gemm_i8_n4")                         \
     X(GEMM_I8_N5, "vkf_gemm_i8_n5")                         \
+    X(GEMM_Q4_K_F16_N4, "vkf_gemm_q4_k_f16_n4")             \
+    X(GEMM_Q4_K_F16_N5, "vkf_gemm_q4_k_f16_n5")             \
     X(GEMV_MFMA_XR_Q4_0_F16, "vkf_gemv_mfma_xr_q4_0_f16_p16") \
     X(GEMV_MFMA_XR_Q4_1_F16, "vkf_gemv_mfma_xr_q4_1_f16_p16") \
     X(GEMV_MFMA_XR_Q4_K_F16_P10, "vkf_gemv_mfma_xr_q4_k_f16_p10") \
@@ -205,6 +207,10 @@ void *real_hip_symbol(const char *name);
 // visible (the vendor libraries may end the process when they find none), or
 // the library or symbol is absent.
 void *vendor_symbol(const char *lib, const char *name);
+
+// Tile width (16·nb columns) of the narrow-tile GEMMs for this grid, 0 if
+// they do not apply (es: bytes per X element).
+uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es);
 
 // Number of compute units of the current device (cached per device).
 int cu_count();

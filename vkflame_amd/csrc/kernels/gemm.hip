@@ -2472,3 +2472,134 @@ VKF_GEMM_N(f16, 2, vkf_f4, 4)
 VKF_GEMM_N(f16, 2, vkf_f4, 5)
 VKF_GEMM_N(i8, 1, vkf_i4, 4)
 VKF_GEMM_N(i8, 1, vkf_i4, 5)
+
+// ---------------------------------------------------------------------------
+// Q4_K weights x fp16 activations on narrow tiles (128 x 16·NB, NB = 4 or
+// 5) for grids of fewer 128 x 128 tiles than CUs, the down projections of a
+// prefill (M = 512, N = 5120, K = 13824: 256 tiles of 128 x 80).  As in the
+// dense narrow kernel the two wave groups take alternate 64-k steps and X
+// moves by direct-to-LDS loads three stages deep; here the weights move the
+// same way, as raw Q4_K bytes, so that every global load of the main loop
+// is counted by hand and none waits for another: per row and 64-k step the
+// super-block header and the step's 32 bytes of codes (three 16-byte
+// pieces; lane L of wave q loads piece L % 3 of row 4·NB·q + L / 3), three
+// steps ahead.  Each step's pieces are decoded (QStage<VKF_Q4_K>: the
+// reference's fp32 value, rounded to fp16) from LDS into a double-buffered
+// fp16 tile in the MFMA layout one step ahead of the MFMAs that read it.
+// LDS: X 3 x 2 x 16 KiB, fp16 weights 2 x 2 x NB·2 KiB, raw 3 x 2 x NB·768
+// bytes (158.5 KiB at NB = 5).  Conditions (host): X K-contiguous, 16-byte
+// aligned, 16-byte rows; W 16-byte aligned rows; K % 256 == 0.
+// ---------------------------------------------------------------------------
+template <int NB>
+struct QnLayout {
+    static constexpr uint32_t XS = 2 * 16384;                      // X, per stage (both groups)
+    static constexpr uint32_t Y16 = 3 * XS, YG = NB * 16 * 128;     // fp16 weights, per group
+    static constexpr uint32_t YS = 2 * YG;
+    static constexpr uint32_t RAW = Y16 + 2 * YS, RG = NB * 16 * 48; // raw Q4_K pieces, per group
+    static constexpr uint32_t RS = 2 * RG;
+    static constexpr uint32_t BYTES = RAW + 3 * RS;
+};
+
+template <int NB>
+__device__ __forceinline__ void gemm_mainloop_q4k_n(const VkfGemmArgs &a, uint32_t r0, uint32_t c0,
+                                                    vkf_f4 acc[2][NB], uint8_t *smem) {
+    using L = QnLayout<NB>;
+    constexpr int RW = 4 * NB;  // weight rows per wave (raw loads and decode)
+    const int wave = threadIdx.x >> 6, g = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
+    const uint32_t npair = a.K / 128;
+    const uint8_t *gx[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t rr = (4 * wq + j) * 8 + (lane >> 3);
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t rx = r0 + rr < a.R ? r0 + rr : a.R - 1;  // rows past the edge: any valid row
+        gx[j] = (const uint8_t *)a.X + (uint64_t)rx * a.ldx * 2 + ch * 16;
+    }
+    // raw pieces: lane L < 3·RW loads piece L % 3 of tile row RW·wq + L / 3
+    const bool rlive = lane < 3 * RW;
+    const uint32_t rrow = RW * wq + (rlive ? (uint32_t)lane / 3 : 0u), rpc = (uint32_t)lane % 3;
+    const uint32_t wrow = c0 + rrow < a.Cn ? c0 + rrow : a.Cn - 1;
+    const uint8_t *wsrc = (const uint8_t *)a.Y + (uint64_t)wrow * a.ldy + 16 * rpc;
+    // decode: lane L < 2·RW of wave q takes half (L & 1) of tile row RW·wq + L / 2
+    const bool dlive = lane < 2 * RW;
+    const uint32_t yr = RW * wq + (dlive ? (uint32_t)lane >> 1 : 0u), yh = lane & 1;
+    auto issue_x = [&](uint32_t p, uint32_t st) {
+        const uint64_t ko = (uint64_t)(2 * p + g) * 128;
+        uint8_t *sx = smem + st * L::XS + g * 16384;
+#pragma unroll
+        for (int j = 0; j < 4; j++) vkf_load_lds16(gx[j] + ko, sx + (4 * wq + j) * 1024);
+    };
+    auto issue_raw = [&](uint32_t p, uint32_t slot) {
+        const uint32_t ks = 2 * p + g;  // this group's 64-k step: super-block ks / 4, code run ks % 4
+        const uint8_t *src = wsrc + 144ull * (ks >> 2) + (rpc ? 32 * (ks & 3) : 0);
+        if (rlive) vkf_load_lds16(src, smem + L::RAW + slot * L::RS + g * L::RG + wq * (3 * RW * 16));
+    };
+    auto decode = [&](uint32_t p, uint32_t slot, uint32_t buf) {
+        if (!dlive) return;
+        const uint32_t ks = 2 * p + g;
+        const uint8_t *rw = smem + L::RAW + slot * L::RS + g * L::RG + yr * 48;
+        QStage<VKF_Q4_K> q;
+        q.hdr = *(const vkf_u4 *)rw;
+        q.qa = *(const vkf_u4 *)(rw + 16);
+        q.qb = *(const vkf_u4 *)(rw + 32);
+        q.j = 2 * (ks & 3) + yh;
+        q.live = c0 + yr < a.Cn;
+        TileRegs t;
+        q.decode(t);
+        uint8_t *sy = smem + L::Y16 + buf * L::YS + g * L::YG + yr * 128;
+#pragma unroll
+        for (int k = 0; k < 4; k++) *(vkf_i4 *)(sy + (((4 * yh + k) ^ (yr & 7)) << 4)) = t.v[k];
+    };
+    // prologue: pair 0 decoded, X of pair 1 and the raw pieces of pair 2 in flight
+    issue_x(0, 0);
+    issue_raw(0, 0);
+    if (npair > 1) issue_raw(1, 1);
+    wait_vm<0>();
+    __syncthreads();
+    decode(0, 0, 0);
+    if (npair > 1) issue_x(1, 1);
+    if (npair > 2) issue_raw(2, 2);
+    uint32_t sx = 0, sr = 1;  // X stage of pair t, raw slot of pair t + 1
+    for (uint32_t t = 0; t < npair; t++) {
+        // X of pair t and the raw pieces of pair t + 1 landed; the previous
+        // iteration's loads (X of t + 1: 4, raw of t + 2: 1 per wave) may stay in flight
+        if (t + 2 < npair) wait_vm<5>();
+        else if (t + 1 < npair) wait_vm<4>();
+        else wait_vm<0>();
+        __syncthreads();
+        const uint32_t sx2 = sx == 0 ? 2 : sx - 1, sr2 = sr == 0 ? 2 : sr - 1;  // (t + 2) % 3, (t + 3) % 3
+        if (t + 2 < npair) issue_x(t + 2, sx2);
+        if (t + 3 < npair) issue_raw(t + 3, sr2);
+        const uint8_t *lx = smem + sx * L::XS + g * 16384;
+        mfma_step_n<2, NB>(lx, smem + L::Y16 + (t & 1) * L::YS + g * L::YG, wq, acc);
+        if (t + 1 < npair) decode(t + 1, sr, (t + 1) & 1);
+        sx = sx == 2 ? 0 : sx + 1;
+        sr = sr == 2 ? 0 : sr + 1;
+    }
+    __syncthreads();  // LDS free for the group sums
+}
+
+template <int NB>
+__device__ __forceinline__ void gemm_q4k_n_body(const VkfGemmArgs &a, uint8_t *smem) {
+    uint32_t r0, c0;
+    gemm_tile_of_n<16 * NB>(r0, c0);
+    vkf_f4 acc[2][NB];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] = vkf_f4{0, 0, 0, 0};
+    const EpiPreN<NB> pre = epi_prefetch_n<NB>(a, r0, c0);
+    gemm_mainloop_q4k_n<NB>(a, r0, c0, acc, smem);
+    vkf_f4 mine[NB];
+    gemm_group_exchange_n<NB>(acc, mine, smem);
+    gemm_epilogue_n<2, NB>(a, r0, c0, mine, smem, pre);
+}
+
+// dynamic LDS: QnLayout<NB>::BYTES
+#define VKF_GEMM_Q4K_N(NB)                                                              \
+    VKF_KERNEL void __launch_bounds__(512) vkf_gemm_q4_k_f16_n##NB(VkfGemmArgs a) {    \
+        extern __shared__ __attribute__((aligned(16))) uint8_t qn_smem[];             \
+        gemm_q4k_n_body<NB>(a, qn_smem);                                                \
+    }
+VKF_GEMM_Q4K_N(4)
+VKF_GEMM_Q4K_N(5)
