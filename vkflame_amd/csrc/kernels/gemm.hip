@@ -539,7 +539,10 @@ struct QStage<VKF_Q4_K> {
             vkf_h8 h;
 #pragma unroll
             for (int e = 0; e < 2; e++) {
-                const uint32_t n = (w[2 * g + e] >> nsh) & 0x0f0f0f0fu;
+                uint32_t n = (w[2 * g + e] >> nsh) & 0x0f0f0f0fu;
+                // n in a register of its own: each code then converts with one
+                // v_cvt_f32_ubyte<k> instead of a bit-field extract and a convert
+                asm volatile("" : "+v"(n));
 #pragma unroll
                 for (int k = 0; k < 4; k++)
                     h[4 * e + k] = vkf_to_f16(fmaf(dsc, (float)((n >> (8 * k)) & 0xffu), -dm));
