@@ -833,7 +833,8 @@ struct QHalf<VKF_Q4_K> {
             vkf_h8 v;
 #pragma unroll
             for (int e = 0; e < 2; e++) {
-                const uint32_t n = (qs[2 * g + e] >> nsh) & 0x0f0f0f0fu;
+                uint32_t n = (qs[2 * g + e] >> nsh) & 0x0f0f0f0fu;
+                asm volatile("" : "+v"(n));  // one v_cvt_f32_ubyte<k> per code (as QStage<VKF_Q4_K>)
 #pragma unroll
                 for (int k = 0; k < 4; k++)
                     v[4 * e + k] = vkf_to_f16(fmaf(dsc, (float)((n >> (8 * k)) & 0xffu), -dm));
