@@ -2240,7 +2240,41 @@ __device__ __forceinline__ void mfma_step_n(const uint8_t *lx, const uint8_t *ly
     __builtin_amdgcn_s_setprio(0);
 }
 
-template <int ES, int NB, class ACC>
+// The same step with Y stored [K, C] (fp16, NN; NB = 4): the step's 64
+// k-rows of the tile's 64 columns lie in LDS as 128-byte rows, row k's
+// 16-byte piece p in slot p ^ 2(k & 3), and each B fragment is read by two
+// ds_read_b64_tr_b16 (the lane layout of mfma_step_trb).
+template <int NB, class ACC>
+__device__ __forceinline__ void mfma_step_n_trb(const uint8_t *lx, const uint8_t *ly, int wq, ACC acc[2][NB]) {
+    static_assert(NB == 4, "NN narrow tiles: 64 columns (8 pieces per k-row)");
+    const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4, sw = li & 7;
+    const int rsub = li >> 2, hb = (li & 1) * 8;  // this lane's row in a 4-row read, half of its piece
+    vkf_i4 fa[2][2], fb[2][NB];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int c = 4 * s + lg;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            fa[s][i] = *(const vkf_i4 *)(lx + (wq * 32 + 16 * i + li) * 128 + ((c ^ sw) << 4));
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const int slot = (2 * j + ((li & 3) >> 1)) ^ (2 * rsub);
+            const uint8_t *q = ly + (32 * s + 8 * lg + rsub) * 128 + slot * 16 + hb;
+            const vkf_i2 lo = lds_read_tr16(q), hi = lds_read_tr16(q + 4 * 128);
+            fb[s][j] = vkf_i4{lo[0], lo[1], hi[0], hi[1]};
+        }
+    }
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) acc[i][j] = mfma_frag<2>(fa[s][i], fb[s][j], acc[i][j]);
+    __builtin_amdgcn_s_setprio(0);
+}
+
+template <int ES, int NB, bool YT, class ACC>
 __device__ __forceinline__ void gemm_mainloop_n(const VkfGemmArgs &a, uint32_t r0, uint32_t c0, ACC acc[2][NB],
                                                 uint8_t *smem) {
     constexpr uint32_t SX = 16384, SG = SX + NB * 16 * 128, SP = 2 * SG;
@@ -2259,20 +2293,29 @@ __device__ __forceinline__ void gemm_mainloop_n(const VkfGemmArgs &a, uint32_t r
     }
 #pragma unroll
     for (int j = 0; j < NYC; j++) {
-        const uint32_t rr = (wq + 4 * j) * 8 + (lane >> 3);
-        const uint32_t ch = (lane & 7) ^ (rr & 7);
-        const uint32_t ry = c0 + rr < a.Cn ? c0 + rr : a.Cn - 1;
-        gy[j] = (const uint8_t *)a.Y + (uint64_t)ry * a.ldy * ES + ch * 16;
+        if constexpr (YT) {
+            // NN: k-row kr of the step (8 per chunk), slot lane & 7 holds the
+            // columns of piece (lane & 7) ^ 2(kr & 3)
+            const uint32_t kr = (wq + 4 * j) * 8 + (lane >> 3), pc = (lane & 7) ^ (2 * (kr & 3));
+            const uint32_t col = c0 + 8 * pc < a.Cn ? c0 + 8 * pc : a.Cn - 8;  // pieces past the edge: any valid one
+            gy[j] = (const uint8_t *)a.Y + ((uint64_t)kr * a.ldy + col) * 2;
+        } else {
+            const uint32_t rr = (wq + 4 * j) * 8 + (lane >> 3);
+            const uint32_t ch = (lane & 7) ^ (rr & 7);
+            const uint32_t ry = c0 + rr < a.Cn ? c0 + rr : a.Cn - 1;
+            gy[j] = (const uint8_t *)a.Y + (uint64_t)ry * a.ldy * ES + ch * 16;
+        }
     }
     // this group's step of pair p into stage st
     auto issue = [&](uint32_t p, uint32_t st) {
         const uint64_t ko = (uint64_t)(2 * p + g) * 128;
+        const uint64_t yo = YT ? (uint64_t)(2 * p + g) * 64 * a.ldy * 2 : ko;
         uint8_t *sx = smem + st * SP + g * SG, *sy = sx + SX;
 #pragma unroll
         for (int j = 0; j < 4; j++) vkf_load_lds16(gx[j] + ko, sx + (4 * wq + j) * 1024);
 #pragma unroll
         for (int j = 0; j < NYC; j++)
-            if (j < ny) vkf_load_lds16(gy[j] + ko, sy + (wq + 4 * j) * 1024);
+            if (j < ny) vkf_load_lds16(gy[j] + yo, sy + (wq + 4 * j) * 1024);
     };
     if (npair > 0) issue(0, 0);
     if (npair > 1) issue(1, 1);
@@ -2288,7 +2331,8 @@ __device__ __forceinline__ void gemm_mainloop_n(const VkfGemmArgs &a, uint32_t r
         __syncthreads();  // every wave's part of pair t is in LDS; pair t - 1's stage is free
         if (t + 2 < npair) issue(t + 2, st == 0 ? 2 : st - 1);
         const uint8_t *lx = smem + st * SP + g * SG;
-        mfma_step_n<ES, NB>(lx, lx + SX, wq, acc);
+        if constexpr (YT) mfma_step_n_trb<NB>(lx, lx + SX, wq, acc);
+        else mfma_step_n<ES, NB>(lx, lx + SX, wq, acc);
         st = st == 2 ? 0 : st + 1;
     }
     __syncthreads();  // LDS free for the group sums
@@ -2448,7 +2492,7 @@ __device__ __forceinline__ void gemm_epilogue_n(const VkfGemmArgs &a, uint32_t r
     }
 }
 
-template <int ES, int NB, class ACC>
+template <int ES, int NB, class ACC, bool YT = false>
 __device__ __forceinline__ void gemm_n_body(const VkfGemmArgs &a0, uint8_t *smem) {
     const VkfGemmArgs a = gemm_batch(a0);
     uint32_t r0, c0;
@@ -2460,7 +2504,7 @@ __device__ __forceinline__ void gemm_n_body(const VkfGemmArgs &a0, uint8_t *smem
         for (int j = 0; j < NB; j++) acc[i][j] = ACC{0, 0, 0, 0};
     EpiPreN<NB> pre{};
     if (!(ES == 1 && (a.flags & VKF_GF_D_I32))) pre = epi_prefetch_n<NB>(a, r0, c0);
-    gemm_mainloop_n<ES, NB>(a, r0, c0, acc, smem);
+    gemm_mainloop_n<ES, NB, YT>(a, r0, c0, acc, smem);
     ACC mine[NB];
     gemm_group_exchange_n<NB>(acc, mine, smem);
     gemm_epilogue_n<ES, NB>(a, r0, c0, mine, smem, pre);
@@ -2476,6 +2520,12 @@ VKF_GEMM_N(f16, 2, vkf_f4, 4)
 VKF_GEMM_N(f16, 2, vkf_f4, 5)
 VKF_GEMM_N(i8, 1, vkf_i4, 4)
 VKF_GEMM_N(i8, 1, vkf_i4, 5)
+// fp16 with Y stored [K, C] (NN), 128 x 64 tiles; Y: 16-byte aligned, ldy % 8
+// == 0, C % 8 == 0
+VKF_KERNEL void __launch_bounds__(512) vkf_gemm_f16_n4t(VkfGemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t gn_smem[];
+    gemm_n_body<2, 4, vkf_f4, true>(a, gn_smem);
+}
 
 // ---------------------------------------------------------------------------
 // Q4_K weights x fp16 activations on narrow tiles (128 x 16·NB, NB = 4 or
