@@ -225,13 +225,17 @@ hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream,
             return launch(id == VKF_K_GEMM_F16 ? VKF_K_GEMM_F16_K2 : VKF_K_GEMM_I8_K2, grid, dim3(512), &g,
                           sizeof(g), stream);
         }
-        // fp16 with Y stored [K, C] (NN): the narrow kernel's 128 x 64 tiles,
-        // Y's k-rows staged as they lie and read back transposed
+        // fp16 with Y stored [K, C] (NN): the narrow kernel's tiles with Y's
+        // k-rows staged as they lie and read back transposed
         if (id == VKF_K_GEMM_F16 && (g.flags & VKF_GF_Y_TRANS) &&
             dma_operand(g.X, g.ldx, (g.flags & VKF_GF_X_TRANS) != 0, g.K, 2) && (g.ldy * 2) % 16 == 0 &&
-            ((uintptr_t)g.Y & 15) == 0 && g.Cn % 8 == 0 && narrow_nb(g, batch, 2) == 4)
-            return launch(VKF_K_GEMM_F16_N4T, dim3((g.Cn + 63) / 64, grid.y, batch), dim3(512), &g, sizeof(g), stream,
-                          kNarrowStages * 2 * (16384 + 4 * 16 * 128));
+            ((uintptr_t)g.Y & 15) == 0 && g.Cn % 8 == 0) {
+            const uint32_t nb = narrow_nb(g, batch, 2);
+            if (nb)
+                return launch(nb == 4 ? VKF_K_GEMM_F16_N4T : VKF_K_GEMM_F16_N5T,
+                              dim3((g.Cn + 16 * nb - 1) / (16 * nb), grid.y, batch), dim3(512), &g, sizeof(g), stream,
+                              kNarrowStages * 2 * (16384 + nb * 16 * 128));
+        }
     }
     return launch(id, grid, dim3(256), &g, sizeof(g), stream);
 }

@@ -2240,13 +2240,21 @@ __device__ __forceinline__ void mfma_step_n(const uint8_t *lx, const uint8_t *ly
     __builtin_amdgcn_s_setprio(0);
 }
 
-// The same step with Y stored [K, C] (fp16, NN; NB = 4): the step's 64
-// k-rows of the tile's 64 columns lie in LDS as 128-byte rows, row k's
-// 16-byte piece p in slot p ^ 2(k & 3), and each B fragment is read by two
-// ds_read_b64_tr_b16 (the lane layout of mfma_step_trb).
+// The same step with Y stored [K, C] (fp16, NN): the step's 64 k-rows of
+// the tile's 16·NB columns lie in LDS as rows of 32·NB bytes, and each B
+// fragment is read by two ds_read_b64_tr_b16 (the lane layout of
+// mfma_step_trb: the 4 rows of a 16-lane read must fall on different
+// banks).  NB = 4: 128-byte rows, row k's 16-byte piece p in slot
+// p ^ 2(k & 3); NB = 5: 160-byte rows as they lie (rows 40 dwords apart
+// already fall on different banks).
+template <int NB>
+__device__ __forceinline__ uint32_t trb_slot(uint32_t p, uint32_t k) {
+    static_assert(NB == 4 || NB == 5, "NN narrow tiles: 64 or 80 columns");
+    return NB == 4 ? p ^ (2 * (k & 3)) : p;
+}
 template <int NB, class ACC>
 __device__ __forceinline__ void mfma_step_n_trb(const uint8_t *lx, const uint8_t *ly, int wq, ACC acc[2][NB]) {
-    static_assert(NB == 4, "NN narrow tiles: 64 columns (8 pieces per k-row)");
+    constexpr int PR = 32 * NB;  // bytes per k-row
     const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4, sw = li & 7;
     const int rsub = li >> 2, hb = (li & 1) * 8;  // this lane's row in a 4-row read, half of its piece
     vkf_i4 fa[2][2], fb[2][NB];
@@ -2258,9 +2266,9 @@ __device__ __forceinline__ void mfma_step_n_trb(const uint8_t *lx, const uint8_t
             fa[s][i] = *(const vkf_i4 *)(lx + (wq * 32 + 16 * i + li) * 128 + ((c ^ sw) << 4));
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-            const int slot = (2 * j + ((li & 3) >> 1)) ^ (2 * rsub);
-            const uint8_t *q = ly + (32 * s + 8 * lg + rsub) * 128 + slot * 16 + hb;
-            const vkf_i2 lo = lds_read_tr16(q), hi = lds_read_tr16(q + 4 * 128);
+            const int slot = trb_slot<NB>(2 * j + ((li & 3) >> 1), rsub);
+            const uint8_t *q = ly + (32 * s + 8 * lg + rsub) * PR + slot * 16 + hb;
+            const vkf_i2 lo = lds_read_tr16(q), hi = lds_read_tr16(q + 4 * PR);
             fb[s][j] = vkf_i4{lo[0], lo[1], hi[0], hi[1]};
         }
     }
@@ -2294,9 +2302,11 @@ __device__ __forceinline__ void gemm_mainloop_n(const VkfGemmArgs &a, uint32_t r
 #pragma unroll
     for (int j = 0; j < NYC; j++) {
         if constexpr (YT) {
-            // NN: k-row kr of the step (8 per chunk), slot lane & 7 holds the
-            // columns of piece (lane & 7) ^ 2(kr & 3)
-            const uint32_t kr = (wq + 4 * j) * 8 + (lane >> 3), pc = (lane & 7) ^ (2 * (kr & 3));
+            // NN: the chunk's 64 lanes fill LDS pieces 64c .. 64c + 63 of the
+            // step's 64 k-rows of 2·NB pieces; piece P = k-row P / (2·NB), slot
+            // P % (2·NB), which holds the columns of piece trb_slot(slot, kr)
+            const uint32_t P = (wq + 4 * j) * 64 + lane, kr = P / (2 * NB);
+            const uint32_t pc = trb_slot<NB>(P % (2 * NB), kr);
             const uint32_t col = c0 + 8 * pc < a.Cn ? c0 + 8 * pc : a.Cn - 8;  // pieces past the edge: any valid one
             gy[j] = (const uint8_t *)a.Y + ((uint64_t)kr * a.ldy + col) * 2;
         } else {
@@ -2520,11 +2530,15 @@ VKF_GEMM_N(f16, 2, vkf_f4, 4)
 VKF_GEMM_N(f16, 2, vkf_f4, 5)
 VKF_GEMM_N(i8, 1, vkf_i4, 4)
 VKF_GEMM_N(i8, 1, vkf_i4, 5)
-// fp16 with Y stored [K, C] (NN), 128 x 64 tiles; Y: 16-byte aligned, ldy % 8
-// == 0, C % 8 == 0
+// fp16 with Y stored [K, C] (NN), 128 x 64 or 128 x 80 tiles; Y: 16-byte
+// aligned, ldy % 8 == 0, C % 8 == 0
 VKF_KERNEL void __launch_bounds__(512) vkf_gemm_f16_n4t(VkfGemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t gn_smem[];
     gemm_n_body<2, 4, vkf_f4, true>(a, gn_smem);
+}
+VKF_KERNEL void __launch_bounds__(512) vkf_gemm_f16_n5t(VkfGemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t gn_smem[];
+    gemm_n_body<2, 5, vkf_f4, true>(a, gn_smem);
 }
 
 // ---------------------------------------------------------------------------
