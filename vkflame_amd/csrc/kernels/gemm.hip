@@ -416,7 +416,9 @@ __device__ __forceinline__ bool dma_ok(const void *P, uint64_t ld, bool trans, u
 }
 
 // One step (128 bytes of K) of the wave's 64x64 tile from swizzled LDS tiles.
-template <int ES, class ACC>
+// PRIO false: no priority raise around the MFMAs (steps whose MFMAs are
+// interleaved with other work by sched_group_barrier hints)
+template <int ES, class ACC, bool PRIO = true>
 __device__ __forceinline__ void mfma_step_swz(const uint8_t *lx, const uint8_t *ly, int wr, int wc, ACC acc[4][4]) {
     const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4, sw = li & 7;
     vkf_i4 fa[2][4], fb[2][4];
@@ -432,7 +434,7 @@ __device__ __forceinline__ void mfma_step_swz(const uint8_t *lx, const uint8_t *
     }
     // raised issue priority for the MFMA burst: when both waves of a SIMD
     // are ready, this wave's MFMAs go first and the matrix pipe stays fed
-    __builtin_amdgcn_s_setprio(1);
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < 2; s++)
 #pragma unroll
@@ -441,7 +443,7 @@ __device__ __forceinline__ void mfma_step_swz(const uint8_t *lx, const uint8_t *
             for (int j = 0; j < 4; j++) {
                 acc[i][j] = mfma_frag<ES>(fa[s][i], fb[s][j], acc[i][j]);
             }
-    __builtin_amdgcn_s_setprio(0);
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
 }
 
 template <int ES, class ACC>
@@ -1476,9 +1478,19 @@ __device__ __forceinline__ void gemm_mainloop_wide(const VkfGemmArgs &a, uint32_
             if (kt + 1 < nk) issue_x(kt + 1, cur ^ 1);
             qf.load(W, a.ldy, a.Cn, c0, a.K, (kt + 2) * 64);
             const uint8_t *lx = smem + cur * GEMM_W_STAGE;
-            mfma_step_swz<2>(lx, lx + 32768, wr, wc, acc);
+            mfma_step_swz<2, vkf_f4, false>(lx, lx + 32768, wr, wc, acc);
             qn.decode(tv);
             store_h(cur ^ 1, tv);
+            // the decode's VALU between the MFMAs: fragment reads first, then
+            // one MFMA and two VALU instructions at a time, the tile stores last
+            __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+#pragma unroll
+            for (int i = 0; i < 32; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
             __syncthreads();
         };
         for (uint32_t kt = 0; kt < nk; kt += 2) {
