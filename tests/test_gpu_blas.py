@@ -115,12 +115,14 @@ def test_gemm_ex_int8_int32(dev, L, handle):
     assert np.array_equal(C.cpu().numpy().T.astype(np.int64), ref)
 
 
-def test_gemm_strided_batched_int8(dev, L, handle):
+@pytest.mark.parametrize("m,n,k", [(64, 48, 96), (256, 200, 512)])
+def test_gemm_strided_batched_int8(dev, L, handle, m, n, k):
     """int8 batch strides in int8 elements (the reference uses 4 bytes,
-    shim/hipblas_shim.cpp:332-334)."""
+    shim/hipblas_shim.cpp:332-334).  256 x 200 x 512: three batches of a
+    grid that fits the CUs with whole K pairs, the narrow-tile kernel."""
     import torch
-    m, n, k, nb = 64, 48, 96, 3
-    rng = np.random.default_rng(seed_for(4, 91))
+    nb = 3
+    rng = np.random.default_rng(seed_for(4, 91) + m)
     A = rng.integers(-127, 128, (nb, m, k)).astype(np.int8)
     Bm = rng.integers(-127, 128, (nb, n, k)).astype(np.int8)
     tA, tB = to_dev(A, dev), to_dev(Bm, dev)
