@@ -257,6 +257,42 @@ def test_linear_fp16_nn_narrow_tiles(dev, M, N, K):
     assert rel_err(E.cpu().numpy().astype(np.float32), O.np_act(3, pre)) <= TOL_F16
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 128), (4100, 4104, 192), (4224, 4352, 256), (4100, 4104, 8192)])
+def test_linear_dense_256_tiles(dev, M, N, K):
+    """Grids of at least one 256x256 tile per CU with K-contiguous operands:
+    the 256 x 256 kernel (eight waves of 128 x 64), ragged rows and columns;
+    int8 always, fp16 from K = 8192 (below, the 128 x 128 kernel).  int8 ->
+    exact int32 (also with integer alpha / beta), fp16 -> fp32 against the
+    float64 product, fp16 out with alpha, beta*C and an activation."""
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd._lib import DTYPE_FP16, DTYPE_FP16_FP32OUT, DTYPE_INT8_INT32OUT
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert -(-M // 256) * -(-N // 256) >= cus
+    rng = np.random.default_rng(seed_for(4, 84) + M + N + K)
+    A = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    Ci = rng.integers(-1000, 1000, (M, N)).astype(np.int32)
+    ref = A.astype(np.int64) @ W.astype(np.int64).T
+    D = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8_INT32OUT, transB=1)
+    D2 = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8_INT32OUT, transB=1,
+                    C=to_dev(Ci, dev), alpha=3, beta=-2)
+    torch.cuda.synchronize()
+    got = D.cpu().numpy().astype(np.int64)
+    assert np.array_equal(got, ref), (M, N, K, int((got != ref).sum()))
+    assert np.array_equal(D2.cpu().numpy(), (3 * ref - 2 * Ci.astype(np.int64)).astype(np.int32))
+    del D, D2
+    Af, Bf, C = _f16(rng, M, K), _f16(rng, N, K), _f16(rng, M, N)
+    reff = Af.astype(np.float64) @ Bf.astype(np.float64).T
+    F = ops.linear(to_dev(Af, dev), to_dev(Bf, dev), M, N, K, DTYPE_FP16_FP32OUT, transB=1)
+    E = ops.linear(to_dev(Af, dev), to_dev(Bf, dev), M, N, K, DTYPE_FP16, transB=1, act=1,
+                   C=to_dev(C, dev), alpha=0.5, beta=0.25)
+    torch.cuda.synchronize()
+    assert rel_err(F.cpu().numpy(), reff) <= TOL_F32
+    pre = (0.5 * reff + 0.25 * C.astype(np.float64)).astype(np.float32)
+    assert rel_err(E.cpu().numpy().astype(np.float32), O.np_act(1, pre)) <= TOL_F16
+
+
 def test_linear_dense_split_k_repeatable(dev):
     """The split-K kernel adds the two groups' fp32 sums in one fixed order:
     the same inputs give the same bits on every call."""

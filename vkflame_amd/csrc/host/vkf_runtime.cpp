@@ -237,6 +237,19 @@ hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream,
                               kNarrowStages * 2 * (16384 + nb * 16 * 128));
         }
     }
+    // grids of at least one 256 x 256 tile per CU, both operands K-contiguous:
+    // the 256 x 256 kernel (half the tile bytes per MAC).  int8 gains on every
+    // such grid measured (4096³ 101 -> 68 us); fp16 from K = 8192 on (4-8 %;
+    // level or slower at K = 4096)
+    if ((id == VKF_K_GEMM_I8 || (id == VKF_K_GEMM_F16 && g.K >= 8192)) && !(g.flags & VKF_GF_X_F16Q) && !g.bpx &&
+        (batch == 1 || ((g.bsx | g.bsy) & 15) == 0)) {
+        const uint32_t es = id == VKF_K_GEMM_F16 ? 2 : 1;
+        const uint64_t t256 = ((uint64_t)g.R + 255) / 256 * (((uint64_t)g.Cn + 255) / 256) * batch;
+        if (t256 >= (uint64_t)cu_count() && dma_operand(g.X, g.ldx, (g.flags & VKF_GF_X_TRANS) != 0, g.K, es) &&
+            dma_operand(g.Y, g.ldy, (g.flags & VKF_GF_Y_TRANS) != 0, g.K, es))
+            return launch(id == VKF_K_GEMM_F16 ? VKF_K_GEMM_F16_B256 : VKF_K_GEMM_I8_B256,
+                          dim3((g.Cn + 255) / 256, (g.R + 255) / 256, batch), dim3(512), &g, sizeof(g), stream);
+    }
     return launch(id, grid, dim3(256), &g, sizeof(g), stream);
 }
 

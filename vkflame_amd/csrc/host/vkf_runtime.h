@@ -124,6 +124,8 @@
     X(GEMM_I8_N5, "vkf_gemm_i8_n5")                         \
     X(GEMM_F16_N4T, "vkf_gemm_f16_n4t")                     \
     X(GEMM_F16_N5T, "vkf_gemm_f16_n5t")                     \
+    X(GEMM_F16_B256, "vkf_gemm_f16_b256")                   \
+    X(GEMM_I8_B256, "vkf_gemm_i8_b256")                     \
     X(GEMM_Q4_K_F16_N4, "vkf_gemm_q4_k_f16_n4")             \
     X(GEMM_Q4_K_F16_N5, "vkf_gemm_q4_k_f16_n5")             \
     X(GEMV_MFMA_XR_Q4_0_F16, "vkf_gemv_mfma_xr_q4_0_f16_p16") \

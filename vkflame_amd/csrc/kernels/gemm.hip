@@ -2389,9 +2389,9 @@ __device__ __forceinline__ void gemm_group_exchange_n(ACC acc[2][NB], ACC mine[N
     __syncthreads();  // LDS free for the epilogue
 }
 
-// Workgroup -> 128 x CT tile, XCD-aware as gemm_tile_of: column tiles dealt
+// Workgroup -> RTT x CT tile, XCD-aware as gemm_tile_of: column tiles dealt
 // to the 8 XCDs round-robin, each XCD running all row tiles of a column.
-template <uint32_t CT>
+template <uint32_t CT, uint32_t RTT = 128>
 __device__ __forceinline__ void gemm_tile_of_n(uint32_t &r0, uint32_t &c0) {
     const uint32_t nc = gridDim.x, nr = gridDim.y, id = blockIdx.x + nc * blockIdx.y;
     const uint32_t full = nc & ~7u;
@@ -2405,7 +2405,7 @@ __device__ __forceinline__ void gemm_tile_of_n(uint32_t &r0, uint32_t &c0) {
         c = full + j / nr;
         r = j % nr;
     }
-    r0 = r * 128;
+    r0 = r * RTT;
     c0 = c * CT;
 }
 
@@ -2683,3 +2683,152 @@ __device__ __forceinline__ void gemm_q4k_n_body(const VkfGemmArgs &a, uint8_t *s
     }
 VKF_GEMM_Q4K_N(4)
 VKF_GEMM_Q4K_N(5)
+
+// ---------------------------------------------------------------------------
+// Dense GEMM on 256 x 256 tiles for grids of at least one such tile per CU
+// (4096³: 256 tiles): half the tile bytes per MAC of the 128 x 128 kernel.
+// 512 threads, eight waves of 128 x 64 (wave w: rows 128(w >> 2), columns
+// 64(w & 3); 8 x 4 fragments of 16 x 16, two waves per SIMD), both operands
+// K-contiguous by direct-to-LDS loads, two stages of 64 KiB (one step in
+// flight while one is multiplied).  The epilogue stages the two 128-row
+// halves one after the other through a 128 x 260 fp32 tile (epi_one's
+// steps per value); D_I32 stores the int32 sums from the registers.
+// ---------------------------------------------------------------------------
+#define GEMM_B256_LDS (128 * 260 * 4)
+
+// rows 128H .. 128H + 127 of the 256 x 256 tile: waves 4H .. 4H + 3 stage
+// their values, all 512 threads store them
+template <int H, class ACC>
+__device__ __forceinline__ void b256_epilogue_half(const VkfGemmArgs &a, uint32_t r0, uint32_t c0,
+                                                   const ACC acc[8][4], uint8_t *smem) {
+    constexpr uint32_t TP = 260;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wr = wave >> 2, wc = wave & 3;
+    const int li = lane & 15, lg = lane >> 4;
+    float *tile = (float *)smem;
+    if (wr == H) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t tr = 16 * i + 4 * lg + e, r = r0 + 128 * H + tr;
+                const uint32_t rc = r < a.R ? r : a.R - 1;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t tc = wc * 64 + 16 * j + li, c = c0 + tc < a.Cn ? c0 + tc : a.Cn - 1;
+                    tile[tr * TP + tc] = epi_one(a, rc, c, (float)acc[i][j][e]);
+                }
+            }
+    }
+    __syncthreads();
+    const bool f32 = (a.flags & VKF_GF_D_F32) != 0;
+    const uint32_t vec = f32 ? 4 : 8;  // elements per 16-byte store
+    const bool vok = (a.ldd % vec) == 0 && (((uintptr_t)a.D & 15) == 0);
+    const uint32_t per_row = 256 / vec;
+    for (uint32_t q = threadIdx.x; q < 128 * per_row; q += 512) {
+        const uint32_t tr = q / per_row, tc = (q % per_row) * vec;
+        const uint32_t r = r0 + 128 * H + tr, c = c0 + tc;
+        if (r >= a.R || c >= a.Cn) continue;
+        const float *src = tile + tr * TP + tc;
+        if (vok && c + vec <= a.Cn) {
+            if (f32) {
+                *(vkf_f4 *)((float *)a.D + (uint64_t)r * a.ldd + c) = *(const vkf_f4 *)src;
+            } else {
+                vkf_h8 hv;
+#pragma unroll
+                for (int k = 0; k < 8; k++) hv[k] = vkf_to_f16(src[k]);
+                *(vkf_h8 *)((_Float16 *)a.D + (uint64_t)r * a.ldd + c) = hv;
+            }
+        } else {
+            for (uint32_t k = 0; k < vec && c + k < a.Cn; k++) {
+                if (f32) ((float *)a.D)[(uint64_t)r * a.ldd + c + k] = src[k];
+                else ((_Float16 *)a.D)[(uint64_t)r * a.ldd + c + k] = vkf_to_f16(src[k]);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+template <int ES, class ACC>
+__device__ __forceinline__ void gemm_b256_body(const VkfGemmArgs &a0, uint8_t *smem) {
+    const VkfGemmArgs a = gemm_batch(a0);
+    uint32_t r0, c0;
+    gemm_tile_of_n<256, 256>(r0, c0);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wr = wave >> 2, wc = wave & 3;
+    const int li = lane & 15, lg = lane >> 4, sw = li & 7;
+    ACC acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = ACC{0, 0, 0, 0};
+    const uint32_t nk = (uint32_t)(((uint64_t)a.K * ES) / 128);
+    const uint8_t *gx[4], *gy[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t rr = (4 * wave + j) * 8 + (lane >> 3);  // 0..255
+        const uint32_t ch = (lane & 7) ^ (rr & 7);
+        const uint32_t rx = r0 + rr < a.R ? r0 + rr : a.R - 1;  // rows past the edge: any valid row
+        const uint32_t ry = c0 + rr < a.Cn ? c0 + rr : a.Cn - 1;
+        gx[j] = (const uint8_t *)a.X + (uint64_t)rx * a.ldx * ES + ch * 16;
+        gy[j] = (const uint8_t *)a.Y + (uint64_t)ry * a.ldy * ES + ch * 16;
+    }
+    auto issue = [&](uint32_t kt, uint32_t st) {
+        uint8_t *sx = smem + st * 65536, *sy = sx + 32768;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            vkf_load_lds16(gx[j] + (uint64_t)kt * 128, sx + (4 * wave + j) * 1024);
+            vkf_load_lds16(gy[j] + (uint64_t)kt * 128, sy + (4 * wave + j) * 1024);
+        }
+    };
+    if (nk > 0) issue(0, 0);
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        wait_vm<0>();  // step kt's loads are the only ones in flight
+        __syncthreads();
+        if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+        const uint8_t *lx = smem + (kt & 1) * 65536, *ly = lx + 32768;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int c = 4 * s + lg;
+            vkf_i4 fa[8], fb[4];
+#pragma unroll
+            for (int i = 0; i < 8; i++) fa[i] = *(const vkf_i4 *)(lx + (wr * 128 + 16 * i + li) * 128 + ((c ^ sw) << 4));
+#pragma unroll
+            for (int j = 0; j < 4; j++) fb[j] = *(const vkf_i4 *)(ly + (wc * 64 + 16 * j + li) * 128 + ((c ^ sw) << 4));
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = mfma_frag<ES>(fa[i], fb[j], acc[i][j]);
+        }
+    }
+    __syncthreads();  // LDS free for the epilogue
+    if constexpr (ES == 1) {
+        if (a.flags & VKF_GF_D_I32) {
+            const int32_t al = __builtin_bit_cast(int32_t, a.alpha), be = __builtin_bit_cast(int32_t, a.beta);
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint32_t r = r0 + wr * 128 + 16 * i + 4 * lg + e, c = c0 + wc * 64 + 16 * j + li;
+                        if (r < a.R && c < a.Cn) {
+                            int32_t v = acc[i][j][e];
+                            if (al != 1 || be != 0)
+                                v = al * v + (be ? be * ((const int32_t *)a.Cin)[(uint64_t)r * a.ldc + c] : 0);
+                            ((int32_t *)a.D)[(uint64_t)r * a.ldd + c] = v;
+                        }
+                    }
+            return;
+        }
+    }
+    b256_epilogue_half<0>(a, r0, c0, acc, smem);
+    b256_epilogue_half<1>(a, r0, c0, acc, smem);
+}
+
+VKF_KERNEL void __launch_bounds__(512) vkf_gemm_f16_b256(VkfGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_B256_LDS];
+    gemm_b256_body<2, vkf_f4>(a, smem);
+}
+VKF_KERNEL void __launch_bounds__(512) vkf_gemm_i8_b256(VkfGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GEMM_B256_LDS];
+    gemm_b256_body<1, vkf_i4>(a, smem);
+}
