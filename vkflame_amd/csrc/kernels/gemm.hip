@@ -2209,7 +2209,7 @@ VKF_KERNEL void __launch_bounds__(64 * SK_WAVES) vkf_gemm_f16_skinny(VkfGemmArgs
 // ---------------------------------------------------------------------------
 // Dense GEMM on narrow tiles for grids of fewer 128 x 128 tiles than CUs:
 // 128 x 16·NB tiles (NB = 4 or 5: 64 or 80 columns), NB picked on the host
-// as the widest tile whose grid still fits one tile per CU (M = 512,
+// as the narrowest tile whose grid still fits one tile per CU (M = 512,
 // N = 5120: 4 x 64 = 256 tiles of 128 x 80, where 128 x 128 tiles give 160
 // and leave 96 CUs idle).  At these sizes a CU's time is its tile traffic
 // over the rate one CU can pull from L2 / MALL, which is set by the bytes it
@@ -2222,12 +2222,10 @@ VKF_KERNEL void __launch_bounds__(64 * SK_WAVES) vkf_gemm_f16_skinny(VkfGemmArgs
 // for NB = 5) keep two pairs of steps in flight while one is multiplied.
 // The group partials meet in LDS, each group then finishing half the tile
 // (int32 exact; fp32 the same bits as one group adding both).  Conditions
-// (host): X and Y K-contiguous, 16-byte aligned,
-// 16-byte rows, K·ES % 256 == 0 (whole pairs of steps).
+// (host): X and Y K-contiguous (or, fp16 only, Y stored [K, C]: the NN
+// variant), 16-byte aligned, 16-byte rows, K·ES % 256 == 0 (whole pairs of
+// steps).  Dynamic LDS: 3 stages x 2 groups x (16 KiB + NB·2 KiB).
 // ---------------------------------------------------------------------------
-template <int NB>
-constexpr uint32_t gn_pair_bytes() { return 2 * (16384 + NB * 16 * 128); }
-#define GN_STAGES 3
 
 template <int ES, int NB, class ACC>
 __device__ __forceinline__ void mfma_step_n(const uint8_t *lx, const uint8_t *ly, int wq, ACC acc[2][NB]) {
@@ -2532,7 +2530,7 @@ __device__ __forceinline__ void gemm_n_body(const VkfGemmArgs &a0, uint8_t *smem
     gemm_epilogue_n<ES, NB>(a, r0, c0, mine, smem, pre);
 }
 
-// dynamic LDS: GN_STAGES x gn_pair_bytes<NB>() (156 KiB for NB = 5)
+// dynamic LDS: 3 x 2 x (16 KiB + NB·2 KiB) (156 KiB for NB = 5)
 #define VKF_GEMM_N(name, ES, ACC, NB)                                                \
     VKF_KERNEL void __launch_bounds__(512) vkf_gemm_##name##_n##NB(VkfGemmArgs a) { \
         extern __shared__ __attribute__((aligned(16))) uint8_t gn_smem[];          \
