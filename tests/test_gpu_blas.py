@@ -138,6 +138,32 @@ def test_gemm_strided_batched_int8(dev, L, handle, m, n, k):
         assert np.array_equal(C[b].cpu().numpy().T.astype(np.int64), ref)
 
 
+def test_gemm_strided_batched_int8_256_tiles(dev, L, handle):
+    """Sixteen batches of 1024 x 1024 x 128 int8: 16 x 16 256x256 tiles, at
+    least one per CU, so the batched grid runs on the 256 x 256 kernel;
+    exact int32 with integer alpha."""
+    import torch
+    m = n = 1024
+    k, nb = 128, 16
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert nb * (m // 256) * (n // 256) >= cus
+    rng = np.random.default_rng(seed_for(4, 92))
+    A = rng.integers(-127, 128, (nb, m, k)).astype(np.int8)
+    Bm = rng.integers(-127, 128, (nb, n, k)).astype(np.int8)
+    tA, tB = to_dev(A, dev), to_dev(Bm, dev)
+    C = torch.zeros((nb, n, m), dtype=torch.int32, device=dev)
+    al, be = ctypes.c_int32(-3), ctypes.c_int32(0)
+    st = L.hipblasGemmStridedBatchedEx(handle, B.OP_T, B.OP_N, m, n, k, ctypes.byref(al), _ptr(tA), B.R_8I, k,
+                                       m * k, _ptr(tB), B.R_8I, k, n * k, ctypes.byref(be), _ptr(C), B.R_32I, m,
+                                       n * m, nb, B.COMPUTE_32I, B.GEMM_DEFAULT)
+    assert st == B.ST_SUCCESS
+    torch.cuda.synchronize()
+    got = C.cpu().numpy()
+    for b in range(nb):
+        ref = -3 * (A[b].astype(np.float64) @ Bm[b].astype(np.float64).T)  # exact: |sum| < 2^53
+        assert np.array_equal(got[b].T.astype(np.float64), ref), b
+
+
 def _lt_matmul(L, dev, A_t, adesc, B_t, bdesc, D_t, ddesc, desc, alpha=1.0, beta=0.0, C_t=None):
     import torch
     h = ctypes.c_void_p()
