@@ -211,7 +211,7 @@ def test_linear_dense_narrow_tiles(dev, M, N, K):
     A = rng.integers(-127, 128, (M, K)).astype(np.int8)
     W = rng.integers(-127, 128, (N, K)).astype(np.int8)
     Ci = rng.integers(-1000, 1000, (M, N)).astype(np.int32)
-    ref = A.astype(np.int64) @ W.astype(np.int64).T
+    ref = (A.astype(np.float64) @ W.astype(np.float64).T).astype(np.int64)  # exact: |sum| < 2^53, through BLAS
     D = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8_INT32OUT, transB=1)
     D2 = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8_INT32OUT, transB=1,
                     C=to_dev(Ci, dev), alpha=3, beta=-2)
@@ -273,7 +273,7 @@ def test_linear_dense_256_tiles(dev, M, N, K):
     A = rng.integers(-127, 128, (M, K)).astype(np.int8)
     W = rng.integers(-127, 128, (N, K)).astype(np.int8)
     Ci = rng.integers(-1000, 1000, (M, N)).astype(np.int32)
-    ref = A.astype(np.int64) @ W.astype(np.int64).T
+    ref = (A.astype(np.float64) @ W.astype(np.float64).T).astype(np.int64)  # exact: |sum| < 2^53, through BLAS
     D = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8_INT32OUT, transB=1)
     D2 = ops.linear(to_dev(A, dev), to_dev(W, dev), M, N, K, DTYPE_INT8_INT32OUT, transB=1,
                     C=to_dev(Ci, dev), alpha=3, beta=-2)
