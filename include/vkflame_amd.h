@@ -123,31 +123,41 @@ int vkflame_dispatch_gemm_q(const void *w, int quant_type, uint64_t row_bytes, c
                             int64_t ldx, float *y, int64_t ldy, int M, int N, int K, void *stream);
 
 /* vkflame_dispatch_gemm_q with a caller-supplied device workspace, in the
- * manner of hipblasLtMatmul's workspace argument.  With Q8_1 activations,
- * M > 16 and packed rows (ldx = K/32*36), a workspace of at least
- * vkflame_gemm_q_workspace_bytes(x_dtype, M, K) bytes, 16-byte aligned,
- * receives the activations decoded once to fp16(d*q) and the fp16-activation
- * GEMM runs on them (from M = 256 with 256-row tiles); without one (NULL or
- * too small) the GEMM decodes activation tiles itself.  Both routes multiply
- * the same fp16 operand values.  vkflame_dispatch_gemm_q allocates the
- * workspace stream-ordered (hipMallocAsync / hipFreeAsync) when the stream
- * is not being captured, and goes without it under capture.  No reference
- * counterpart as an entry point: the workspace stands for the activation
- * temporary of the reference's mul_mat path (shim/hip_runtime_shim.cpp:1102-1172). */
+ * manner of hipblasLtMatmul's workspace argument, 16-byte aligned, of at
+ * least vkflame_gemm_q_workspace_bytes(quant_type, x_dtype, M, N, K) bytes;
+ * without one (NULL or too small) each route below runs its no-workspace
+ * form.  Two routes use it:
+ *  - Q8_1 activations, M > 16, packed rows (ldx = K/32*36): M*K*2 bytes
+ *    receive the activations decoded once to fp16(d*q) and the
+ *    fp16-activation GEMM runs on them (from M = 256 with 256-row tiles);
+ *    without it the GEMM decodes activation tiles itself.  Both multiply the
+ *    same fp16 operand values.
+ *  - Q4_K (K > 5120) and Q4_0 / Q4_1 (K > 4096) weights, fp16 activations,
+ *    2 <= M <= 16, at most 8 K slices (of 20 / 16 256-k groups): S*M*N*4
+ *    bytes hold the partial products of S K slices, which run side by side
+ *    on the matrix-core GEMV and are added in slice order by a second
+ *    launch; without it the slices run one launch after another.
+ * vkflame_dispatch_gemm_q allocates the workspace stream-ordered
+ * (hipMallocAsync / hipFreeAsync) when the stream is not being captured,
+ * and goes without it under capture.  No reference counterpart as an entry
+ * point: the workspace stands for the temporaries of the reference's mul_mat
+ * path (shim/hip_runtime_shim.cpp:1102-1172). */
 int vkflame_dispatch_gemm_q_ws(const void *w, int quant_type, uint64_t row_bytes, const void *x, int x_dtype,
                                int64_t ldx, float *y, int64_t ldy, int M, int N, int K, void *workspace,
                                size_t workspace_bytes, void *stream);
 /* Workspace bytes vkflame_dispatch_gemm_q_ws uses for these arguments (0: none). */
-size_t vkflame_gemm_q_workspace_bytes(int x_dtype, int M, int K);
+size_t vkflame_gemm_q_workspace_bytes(int quant_type, int x_dtype, int M, int N, int K);
 
-/* vkflame_dispatch_gemm_q that allocates nothing: the one scratch buffer of
- * that entry point (the fp16 copy of Q8_1 activations at M > 16, M*K*2 bytes)
- * is a fixed device array of VKFLAME_NOALLOC_SCRATCH_BYTES inside the library,
- * one per GPU, held until the process ends.  No reference counterpart: it is
- * for callers that cannot call hipMalloc (code under HIP graph capture, tight
- * serving loops, harnesses that forbid allocation).  Same arguments and
- * results as vkflame_dispatch_gemm_q; returns hipErrorInvalidValue (and says
- * so on stderr) when M*K*2 exceeds the array.  Every call on one GPU shares
+/* vkflame_dispatch_gemm_q that allocates nothing: the scratch buffer of
+ * that entry point (the fp16 copy of Q8_1 activations at M > 16, M*K*2 bytes;
+ * the K-slice partials of the GEMV, S*M*N*4 bytes) is a fixed device array of
+ * VKFLAME_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until
+ * the process ends.  No reference counterpart: it is for callers that cannot
+ * call hipMalloc (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation).  Same arguments and results as
+ * vkflame_dispatch_gemm_q; returns hipErrorInvalidValue (and says so on
+ * stderr) when M*K*2 exceeds the array (a GEMV whose K-slice partials exceed
+ * it runs its slices one launch after another instead).  Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (different streams, or
  * threads) race and must be ordered by the caller.  The first call on a device
  * looks the array up (hipGetSymbolAddress); make it outside graph capture. */

@@ -57,8 +57,10 @@ static void c_abi() {
     CHECK(vkflame_dispatch_linear(p, p, nullptr, p, 4, 4, 4, VKF_DTYPE_FP16, 0, 0, 7, nullptr, nullptr, nullptr) == 1);
     float bad = -1.0f;
     CHECK(vkflame_dispatch_linear(p, p, nullptr, p, 4, 4, 4, VKF_DTYPE_INT8, 0, 1, 0, &bad, nullptr, nullptr) == 1);
-    CHECK(vkflame_gemm_q_workspace_bytes(VKF_DTYPE_Q8_1, 512, 5120) == (size_t)512 * 5120 * 2);
-    CHECK(vkflame_gemm_q_workspace_bytes(VKF_DTYPE_Q8_1, 16, 5120) == 0);
+    CHECK(vkflame_gemm_q_workspace_bytes(VKF_DEQUANT_Q6_K, VKF_DTYPE_Q8_1, 512, 4096, 5120) == (size_t)512 * 5120 * 2);
+    CHECK(vkflame_gemm_q_workspace_bytes(VKF_DEQUANT_Q6_K, VKF_DTYPE_Q8_1, 16, 4096, 5120) == 0);
+    CHECK(vkflame_gemm_q_workspace_bytes(VKF_DEQUANT_Q4_K, VKF_DTYPE_FP16, 8, 5120, 13824) == (size_t)3 * 8 * 5120 * 4);
+    CHECK(vkflame_gemm_q_workspace_bytes(VKF_DEQUANT_Q4_K, VKF_DTYPE_FP16, 8, 5120, 5120) == 0);
     CHECK(vkflame_noalloc_scratch_bytes() == VKFLAME_NOALLOC_SCRATCH_BYTES);
     CHECK(vkflame_dispatch_gemm_q_noalloc(p, VKF_DEQUANT_Q6_K, 0, p, VKF_DTYPE_Q8_1, 0, (float *)p, 0, 2048, 64, 8192,
                                           nullptr) == 1);

@@ -190,8 +190,27 @@ def test_c_abi_rejects_bad_arguments():
     assert L.vkflame_stream_read(P(16), 32, None, s) == 1                     # no sink
     assert L.vkflame_stream_read(None, 0, None, s) == 0                       # empty: no-op
     ws = L.vkflame_gemm_q_workspace_bytes
-    assert ws(VL.DTYPE_Q8_1, 512, 5120) == 512 * 5120 * 2
-    assert ws(VL.DTYPE_Q8_1, 16, 5120) == 0 and ws(VL.DTYPE_FP16, 512, 5120) == 0 and ws(VL.DTYPE_Q8_1, 64, 100) == 0
+    q4_0, q4k, q6k = 0, 4, 6  # VKF_DEQUANT_*
+    assert ws(q6k, VL.DTYPE_Q8_1, 512, 4096, 5120) == 512 * 5120 * 2
+    assert ws(q6k, VL.DTYPE_Q8_1, 16, 4096, 5120) == 0 and ws(q6k, VL.DTYPE_FP16, 512, 4096, 5120) == 0
+    assert ws(q6k, VL.DTYPE_Q8_1, 64, 4096, 100) == 0
+    # K-slice partials of the matrix-core GEMV: S = ceil(K/256 / 20) (Q4_K), ceil(K/256 / 16) (Q4_0 / Q4_1)
+    assert ws(q4k, VL.DTYPE_FP16, 8, 5120, 13824) == 3 * 8 * 5120 * 4
+    assert ws(q4k, VL.DTYPE_FP16, 16, 5120, 5376) == 2 * 16 * 5120 * 4
+    assert ws(q4_0, VL.DTYPE_FP16, 4, 4096, 11008) == 3 * 4 * 4096 * 4
+    assert ws(q4_0, VL.DTYPE_FP16, 16, 4096, 4608) == 2 * 16 * 4096 * 4
+    assert ws(q4k, VL.DTYPE_FP16, 8, 13824, 5120) == 0      # one workgroup's waves hold K = 5120
+    assert ws(q4_0, VL.DTYPE_FP16, 4, 11008, 4096) == 0
+    # one LDS-image launch holds 33 (Q4_K) / 35 (Q4_0) groups of 8 rows, 16 / 17 of 16 rows
+    assert ws(q4k, VL.DTYPE_FP16, 8, 5120, 256 * 33) == 0 and ws(q4k, VL.DTYPE_FP16, 8, 5120, 256 * 34) > 0
+    assert ws(q4_0, VL.DTYPE_FP16, 8, 4096, 256 * 35) == 0 and ws(q4_0, VL.DTYPE_FP16, 8, 4096, 256 * 36) > 0
+    assert ws(q4_0, VL.DTYPE_FP16, 16, 4096, 256 * 17) == 0
+    assert ws(q4k, VL.DTYPE_FP16, 1, 5120, 13824) == 0      # M = 1: the dot GEMV
+    assert ws(q4k, VL.DTYPE_FP16, 17, 5120, 13824) == 0     # M > 16: the GEMM
+    assert ws(q4k, VL.DTYPE_FP32, 8, 5120, 13824) == 0      # fp16 activations only
+    assert ws(q6k, VL.DTYPE_FP16, 8, 5120, 13824) == 0
+    assert ws(q4k, VL.DTYPE_FP16, 8, 5120, 256 * 161) == 0  # more than 8 slices
+    assert ws(q4k, VL.DTYPE_FP16, 8, 5120, 256 * 160) == 8 * 8 * 5120 * 4
     qws = L.vkflame_dispatch_gemm_q_ws
     assert qws(P(16), 4, 0, P(16), 1, 0, P(16), 0, 1, 8, 300, None, 0, s) == 1     # K % 256
     assert qws(P(16), 6, 0, P(18), 11, 0, P(16), 0, 64, 8, 256, P(16), 1 << 20, s) == 1  # Q8_1 x not 4-aligned

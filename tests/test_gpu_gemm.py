@@ -475,9 +475,9 @@ def test_gemm_q_q8_1_workspace_paths(dev, qt, M, K):
     x = np.random.default_rng(seed_for(3, 80 + qt)).normal(0, 1, (M, K)).astype(np.float32)
     xq = O.np_quantize_q8_1(x).reshape(M, -1)
     wd, xd = to_dev(w, dev), to_dev(xq, dev)
-    assert L.lib().vkflame_gemm_q_workspace_bytes(L.DTYPE_Q8_1, M, K) == M * K * 2
-    assert L.lib().vkflame_gemm_q_workspace_bytes(L.DTYPE_Q8_1, 16, K) == 0
-    assert L.lib().vkflame_gemm_q_workspace_bytes(L.DTYPE_FP16, M, K) == 0
+    assert L.lib().vkflame_gemm_q_workspace_bytes(qt, L.DTYPE_Q8_1, M, N, K) == M * K * 2
+    assert L.lib().vkflame_gemm_q_workspace_bytes(qt, L.DTYPE_Q8_1, 16, N, K) == 0
+    assert L.lib().vkflame_gemm_q_workspace_bytes(qt, L.DTYPE_FP16, M, N, K) == 0
     y_ws = ops.gemm_q(wd, qt, xd, N, K)
     y_tile = ops.gemm_q(wd, qt, xd, N, K, workspace=False)
     y_lib = torch.empty((M, N), dtype=torch.float32, device=dev)

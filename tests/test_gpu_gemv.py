@@ -268,7 +268,9 @@ MFMA_TYPES = [O.Q4_K, O.Q5_K, O.Q4_0, O.Q4_1, O.Q8_0, O.Q5_0]
 def test_gemv_mfma(dev, qt, M, N, K):
     """Q4_K, Q5_K, Q4_0, Q4_1, Q8_0, Q5_0 x fp16 at 2 <= M <= 16 on the matrix cores: 8- and
     16-row activation images, every K-split width the host picks, and
-    K = 13824, which runs as several K-slice launches accumulating into y."""
+    K = 13824, which runs as several K-slice launches accumulating into y
+    (Q5_K, Q8_0, Q5_0) or, for Q4_K, Q4_0 and Q4_1, as K slices side by side
+    in one launch with a workspace for their partials."""
     from vkflame_amd import ops
     w = O.gen_weight(qt, N, K, seed_for(2, 60 + M + 20 * qt))
     xa, x64 = _x("f16", M, K, seed_for(2, 70 + M))
@@ -281,8 +283,8 @@ def test_gemv_mfma(dev, qt, M, N, K):
 @pytest.mark.parametrize("M", [3, 16])
 def test_gemv_mfma_many_rounds(dev, qt, K, M):
     """The register-activation kernel on more 16-row tiles than two rounds of
-    one workgroup per CU (the weights of the round after next staged in LDS
-    while a round computes) with a ragged last tile; K = 2304 leaves some
+    one workgroup per CU (the next round's weights requested while a round's
+    partial tiles are added) with a ragged last tile; K = 2304 leaves some
     waves without groups."""
     import torch
     from vkflame_amd import ops
@@ -292,6 +294,60 @@ def test_gemv_mfma_many_rounds(dev, qt, K, M):
     xa, x64 = _x("f16", M, K, seed_for(2, 95 + M))
     y = ops.gemm_q(to_dev(w, dev), qt, to_dev(xa, dev), N, K).cpu().numpy()
     assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32
+
+
+KS_CASES = [(O.Q4_K, 256 * 34), (O.Q4_K, 13824), (O.Q4_K, 256 * 160), (O.Q4_0, 256 * 36), (O.Q4_0, 11008),
+            (O.Q4_1, 11008), (O.Q4_1, 256 * 128)]
+
+
+@pytest.mark.parametrize("qt,K", KS_CASES, ids=[f"{O.QNAMES[q]}-{k}" for q, k in KS_CASES])
+@pytest.mark.parametrize("M", [2, 7, 16])
+@pytest.mark.parametrize("N", [77, "rounds"])
+def test_gemv_mfma_k_slices(dev, qt, K, M, N):
+    """Long K on the register-activation kernel as K slices side by side in
+    one launch (2 to 8 slices: K/256 = 34 and 36 groups, 13824, 11008, and
+    the longest K the route takes, 8 slices of 20 or 16 groups), each
+    workgroup on one slice, the partials added in slice order by a second
+    launch: against the float64 product per activation row, against the
+    no-workspace route (K-slice launches one after another) within the same
+    tolerance, and bit for bit between two calls.  N = "rounds" gives every
+    workgroup more than one 16-row tile and a ragged last tile."""
+    import torch
+    from vkflame_amd import ops
+    from vkflame_amd import _lib as L
+    if N == "rounds":
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        N = 16 * cus + 40 if K <= 13824 else 600
+    S = L.lib().vkflame_gemm_q_workspace_bytes(qt, L.DTYPE_FP16, M, N, K) // (M * N * 4)
+    assert 2 <= S <= 8, S
+    print(f"k slices: {O.QNAMES[qt]} {N}x{K} M={M} S={S}", flush=True)
+    w = O.gen_weight(qt, N, K, seed_for(2, 110 + M + 20 * qt))
+    xa, x64 = _x("f16", M, K, seed_for(2, 115 + M))
+    wd, xd = to_dev(w, dev), to_dev(xa, dev)
+    y = ops.gemm_q(wd, qt, xd, N, K)
+    y2 = ops.gemm_q(wd, qt, xd, N, K)
+    y_seq = ops.gemm_q(wd, qt, xd, N, K, workspace=False)
+    torch.cuda.synchronize()
+    a, b = y.cpu().numpy(), y2.cpu().numpy()
+    assert bits_equal(a, b), first_mismatch(a, b)
+    assert _per_row_err(a, x64, w, qt, N, K) <= TOL_F32
+    assert _per_row_err(y_seq.cpu().numpy(), x64, w, qt, N, K) <= TOL_F32
+    assert max(rel_err(a[m], y_seq.cpu().numpy()[m]) for m in range(M)) <= TOL_F32
+
+
+def test_gemv_mfma_k_slices_strided_output(dev):
+    """The slice sum writes y at its row stride and leaves the padding."""
+    import torch
+    from vkflame_amd import ops
+    N, K, M = 300, 13824, 5
+    w = O.gen_weight(O.Q4_K, N, K, seed_for(2, 140))
+    xa, x64 = _x("f16", M, K, seed_for(2, 141))
+    ybig = torch.full((M, N + 24), 7.0, device=dev)
+    ops.gemm_q(to_dev(w, dev), O.Q4_K, to_dev(xa, dev), N, K, out=ybig[:, :N])
+    torch.cuda.synchronize()
+    yb = ybig.cpu().numpy()
+    assert np.all(yb[:, N:] == 7.0)
+    assert _per_row_err(yb[:, :N], x64, w, O.Q4_K, N, K) <= TOL_F32
 
 
 @pytest.mark.parametrize("M", [2, 5, 8, 9, 16])

@@ -43,8 +43,8 @@ def sanity_binary(tmp_path_factory):
         'extern "C" size_t vkflame_noalloc_scratch_bytes(void) { return VKFLAME_NOALLOC_SCRATCH_BYTES; }\n'
         'extern "C" int vkflame_dispatch_gemm_q_noalloc(const void *w, int qt, uint64_t rb, const void *x, int xd,\n'
         '    int64_t ldx, float *y, int64_t ldy, int M, int N, int K, void *s) {\n'
-        '  size_t need = vkflame_gemm_q_workspace_bytes(xd, M, K);\n'
-        '  if (need > VKFLAME_NOALLOC_SCRATCH_BYTES) return 1;\n'
+        '  size_t need = vkflame_gemm_q_workspace_bytes(qt, xd, M, N, K);\n'
+        '  if (M > 16 && need > VKFLAME_NOALLOC_SCRATCH_BYTES) return 1;\n'
         '  return vkflame_dispatch_gemm_q_ws(w, qt, rb, x, xd, ldx, y, ldy, M, N, K, nullptr, 0, s); }\n')
     so = str(out / "stubs.o")
     subprocess.run([*cxx, f"-I{ROOT}/include", "-c", str(stub), "-o", so], check=True, capture_output=True)

@@ -56,7 +56,7 @@ def lib() -> ctypes.CDLL:
     L.vkflame_quantize_q8_1.argtypes = [P, P, I, I, I64, P]
     L.vkflame_dispatch_gemm_q.argtypes = [P, I, U64, P, I, I64, P, I64, I, I, I, P]
     L.vkflame_dispatch_gemm_q_ws.argtypes = [P, I, U64, P, I, I64, P, I64, I, I, I, P, ctypes.c_size_t, P]
-    L.vkflame_gemm_q_workspace_bytes.argtypes = [I, I, I]
+    L.vkflame_gemm_q_workspace_bytes.argtypes = [I, I, I, I, I]
     L.vkflame_gemm_q_workspace_bytes.restype = ctypes.c_size_t
     L.vkflame_dispatch_gemm_q_noalloc.argtypes = [P, I, U64, P, I, I64, P, I64, I, I, I, P]
     L.vkflame_noalloc_scratch_bytes.argtypes = []

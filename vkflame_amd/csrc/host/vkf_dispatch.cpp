@@ -61,6 +61,28 @@ VkfKernelId gemm_kernel(int qt, int xk) {
 // weights, fp16 / fp32 activations, M <= 4.  Chunks are 64 elements; the
 // chunk loads need the row starts aligned as below (36-, 40-, 68-, 144- and
 // 176-byte chunk groups).
+// K-sliced register-activation GEMV (kernels/gemv_mfma.hip gemv_mfma_xr, KS):
+// Q4_K (ten waves of two 256-k groups) and Q4_0 / Q4_1 (sixteen waves of
+// one) with fp16 activations, 2 <= M <= 16, on up to kMaxKSlices slices, at
+// a K too long for one workgroup's waves to hold (Q4_K above 5120, Q4_0 /
+// Q4_1 above 4096) whose activation image does not fit one launch of the
+// LDS-image kernel either (160 KiB of LDS on gfx950; 5120x5376 Q4_K M = 8:
+// 11.5 us in one LDS-image launch, 13.6 us on two K slices; 5120x13824
+// M = 8 / 16: 27.9 / 44.4 us in two LDS-image launches, 17.5 / 18.6 us on
+// three K slices).  Returns the slice count (0: not this route); the
+// partials take S*M*N floats of workspace.
+constexpr uint32_t kMaxKSlices = 8;
+constexpr size_t kLdsGfx950 = 160 * 1024;
+uint32_t ks_slices(int qt, int x_dtype, int M, int K) {
+    if (x_dtype != VKF_DTYPE_FP16 || M < 2 || M > 16 || K <= 0 || (K % 256) != 0) return 0;
+    const uint32_t per = qt == VKF_Q4_K ? 20 : (qt == VKF_Q4_0 || qt == VKF_Q4_1) ? 16 : 0;
+    const uint32_t nsb = (uint32_t)(K / 256);
+    const size_t per_group = (size_t)(M <= 8 ? 8 : 16) * (qt == VKF_Q4_K ? 544 : 512);  // LDS image, 256 k
+    if (per == 0 || nsb <= per || nsb <= (kLdsGfx950 - kMfmaRed) / per_group) return 0;
+    const uint32_t S = cdiv(nsb, per);
+    return S <= kMaxKSlices ? S : 0;
+}
+
 constexpr int kDotWaves = 16;
 // LDS image per workgroup: 8 planes of 4 KiB per reserved activation row
 // plus a 4 KiB table of per-chunk scales and sums (kernels/gemv_dot.hip),
@@ -163,15 +185,18 @@ int vkflame_quantize_q8_1(const float *x, void *dst, int M, int K, int64_t ldx, 
     return vkf::launch(VKF_K_QUANT_Q8_1, dim3(cdiv((uint64_t)M * K, 256)), dim3(256), a, S(stream));
 }
 
-size_t vkflame_gemm_q_workspace_bytes(int x_dtype, int M, int K) {
+size_t vkflame_gemm_q_workspace_bytes(int qt, int x_dtype, int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    // K-slice partials of the register-activation GEMV
+    if (const uint32_t S = ks_slices(qt, x_dtype, M, K)) return (size_t)S * (size_t)M * (size_t)N * 4;
     // fp16 copy of Q8_1 activations for the prefill GEMM
-    if (x_dtype != VKF_DTYPE_Q8_1 || M <= 16 || K <= 0 || (K % 32) != 0) return 0;
+    if (x_dtype != VKF_DTYPE_Q8_1 || M <= 16 || (K % 32) != 0) return 0;
     return (size_t)M * (size_t)K * 2;
 }
 
 int vkflame_dispatch_gemm_q(const void *w, int qt, uint64_t row_bytes, const void *x, int x_dtype, int64_t ldx,
                             float *y, int64_t ldy, int M, int N, int K, void *stream) {
-    const size_t ws = vkflame_gemm_q_workspace_bytes(x_dtype, M, K);
+    const size_t ws = vkflame_gemm_q_workspace_bytes(qt, x_dtype, M, N, K);
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (ws == 0 || N <= 0 || hipStreamIsCapturing(S(stream), &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
         return vkflame_dispatch_gemm_q_ws(w, qt, row_bytes, x, x_dtype, ldx, y, ldy, M, N, K, nullptr, 0, stream);
@@ -261,6 +286,25 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
                 const VkfKernelId k = xrk ? VKF_K_GEMV_MFMA_XR_Q4_K_F16_P10
                                           : mf == 1 ? VKF_K_GEMV_MFMA_XR_Q4_0_F16 : VKF_K_GEMV_MFMA_XR_Q4_1_F16;
                 return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * P), a, S(stream), 1024 * P);
+            }
+            // longer K on K slices, one slice per workgroup, the partials in
+            // the workspace summed in slice order by a second launch
+            const uint32_t ns = xk == 0 ? ks_slices(qt, x_dtype, M, K) : 0;
+            if (ns && workspace && aligned(workspace, 16) &&
+                workspace_bytes >= vkflame_gemm_q_workspace_bytes(qt, x_dtype, M, N, K)) {
+                const uint32_t tiles = cdiv(N, 16), cus = (uint32_t)vkf::cu_count(), P = mf == 0 ? 10 : 16;
+                const uint32_t lanes = cus / ns == 0 ? 1 : (tiles < cus / ns ? tiles : cus / ns);
+                const VkfKernelId k = mf == 0   ? VKF_K_GEMV_MFMA_XR_Q4_K_F16_P10_KS
+                                      : mf == 1 ? VKF_K_GEMV_MFMA_XR_Q4_0_F16_KS
+                                                : VKF_K_GEMV_MFMA_XR_Q4_1_F16_KS;
+                VkfGemvArgs b = a;
+                b.y = (float *)workspace;
+                b.ldy = (uint64_t)N;
+                b.flags = ns << 8;
+                const int rc = vkf::launch(k, dim3(ns * lanes), dim3(64 * P), b, S(stream), 1024 * P);
+                if (rc) return rc;
+                VkfSplitSumArgs r{(const float *)workspace, y, (uint64_t)ldy, (uint32_t)M, (uint32_t)N, ns, 0u};
+                return vkf::launch(VKF_K_GEMV_SPLIT_SUM, dim3(cdiv(N, 256), M), dim3(256), r, S(stream));
             }
             const uint32_t nsb = (uint32_t)(K / 256), cap = (uint32_t)((vkf::max_lds() - kMfmaRed) / per_group);
             const uint32_t slices = cdiv(nsb, cap), per = cdiv(nsb, slices);
@@ -354,7 +398,7 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
         g.flags = VKF_GF_D_F32;
         return vkf::launch(VKF_K_GEMM_Q8_0_Q81_I8, dim3(cdiv(N, 128), cdiv(M, 128)), dim3(512), g, S(stream));
     }
-    if (xk == 2 && workspace && workspace_bytes >= vkflame_gemm_q_workspace_bytes(x_dtype, M, K) &&
+    if (xk == 2 && workspace && workspace_bytes >= vkflame_gemm_q_workspace_bytes(qt, x_dtype, M, N, K) &&
         aligned(workspace, 16) && ldx == (int64_t)(K / 32) * 36) {
         // decode the activations once (fp16(d*q), the value the Q8_1 GEMM's
         // own tile decode produces) and run the fp16-activation GEMM

@@ -3,7 +3,8 @@
 // graph capture, tight serving loops, harnesses that forbid hipMalloc).
 //
 // vkflame_dispatch_gemm_q allocates one scratch buffer, stream-ordered: the
-// fp16 copy of Q8_1 activations at M > 16 (M*K*2 bytes).  Here that buffer
+// fp16 copy of Q8_1 activations at M > 16 (M*K*2 bytes), or the K-slice
+// partials of the register-activation GEMV (S*M*N*4 bytes).  Here that buffer
 // is a file-scope device array, `scratch`, of kScratchBytes; each GPU the
 // library runs on holds its own copy until the process ends.  Host code
 // never passes the array's name to a kernel (on the host it is only a
@@ -69,8 +70,10 @@ size_t vkflame_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 int vkflame_dispatch_gemm_q_noalloc(const void *w, int quant_type, uint64_t row_bytes, const void *x, int x_dtype,
                                     int64_t ldx, float *y, int64_t ldy, int M, int N, int K, void *stream) {
-    const size_t need = vkflame_gemm_q_workspace_bytes(x_dtype, M, K);
-    if (need == 0)  // no scratch on this route: the same call as vkflame_dispatch_gemm_q
+    const size_t need = vkflame_gemm_q_workspace_bytes(quant_type, x_dtype, M, N, K);
+    // no scratch on this route, or GEMV K-slice partials beyond the array (the
+    // GEMV then runs its slices one launch after another, as with no workspace)
+    if (need == 0 || (M <= 16 && need > kScratchBytes))
         return vkflame_dispatch_gemm_q_ws(w, quant_type, row_bytes, x, x_dtype, ldx, y, ldy, M, N, K, nullptr, 0,
                                           stream);
     if (need > kScratchBytes) {

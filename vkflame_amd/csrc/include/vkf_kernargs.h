@@ -75,6 +75,15 @@ struct VkfGemvArgs {
     uint32_t flags; // bit 0: y += (accumulate) instead of y =
 };
 
+// Sum of the K-slice partials of a GEMV: y[m, n] = sum over s < S, in order,
+// of part[(s*M + m)*N + n].
+struct VkfSplitSumArgs {
+    const float *part;
+    float *y;
+    uint64_t ldy;   // elements
+    uint32_t M, N, S, pad;
+};
+
 // Dense GEMM core, both operands K-contiguous:
 //   D[r, c] = epi( sum_k X[r, k] * Y[c, k] )   r < R, c < C
 // X row r at X + r*ldx, Y row c at Y + c*ldy, D element at D + r*ldd + c.
@@ -134,6 +143,7 @@ inline void vkf_gemm_set_int_scalars(VkfGemmArgs &g, int32_t alpha, int32_t beta
 static_assert(sizeof(VkfDequantArgs) == 24, "VkfDequantArgs layout");
 static_assert(sizeof(VkfQuantizeArgs) == 32, "VkfQuantizeArgs layout");
 static_assert(sizeof(VkfStreamArgs) == 24, "VkfStreamArgs layout");
+static_assert(sizeof(VkfSplitSumArgs) == 40, "VkfSplitSumArgs layout");
 static_assert(sizeof(VkfQuantRowsArgs) == 48, "VkfQuantRowsArgs layout");
 static_assert(sizeof(VkfGemvArgs) == 64, "VkfGemvArgs layout");
 static_assert(sizeof(VkfGemmArgs) == 176, "VkfGemmArgs layout");

@@ -833,16 +833,27 @@ VKF_GEMV_MFMA(q5_0, GF_Q5_0)
 // next round's weights, and the P partial tiles meet in LDS, where wave 0
 // adds them in wave order.  Rows >= M of the MFMA operand repeat row M - 1
 // (MR = M rounded up to 4, 8 or 16) and feed discarded outputs.
+//
+// K slices (KS, for K longer than P waves hold): the S = flags bits 8..15
+// slices [s*G/S, (s+1)*G/S) of the groups go to different workgroups;
+// workgroup b takes slice b % S of the tiles b / S, b / S + gridDim.x / S,
+// ... (gridDim.x a multiple of S) and stores its partial tile to
+// y[(s*M + m)*ldy + n] (y is then the caller's workspace), which
+// vkf_gemv_split_sum adds up in slice order.
 // ---------------------------------------------------------------------------
-template <int F, uint32_t MR, int NG, int P>
+template <int F, uint32_t MR, int NG, int P, bool KS>
 __device__ __forceinline__ void gemv_mfma_xr(const VkfGemvArgs &a, unsigned char *smem) {
     const uint32_t nsb = a.K / 256;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 15, lg = lane >> 4;
     const uint32_t ntiles = (a.N + 15) / 16;
-    // this wave's groups [g0, g0 + ng), ng <= NG (the host's choice of P)
-    const uint32_t g0 = wave * nsb / P, ng = (wave + 1) * nsb / P - g0;
+    const uint32_t S = KS ? (a.flags >> 8) & 0xffu : 1u, slice = KS ? blockIdx.x % S : 0u;
+    const auto tstep = [&]() { return KS ? gridDim.x / S : gridDim.x; };  // tiles between rounds
+    // this wave's groups [g0, g0 + ng), ng <= NG (the host's choice of P and S)
+    const uint32_t sg0 = slice * nsb / S, sgn = (slice + 1) * nsb / S - sg0;
+    const uint32_t g0 = KS ? sg0 + wave * sgn / P : wave * nsb / P;
+    const uint32_t ng = KS ? sg0 + (wave + 1) * sgn / P - g0 : (wave + 1) * nsb / P - g0;
     const uint32_t arow = li < (int)MR ? li : li & (MR - 1);
     const uint32_t xrow = arow < a.M ? arow : a.M - 1;
     const _Float16 *xp = (const _Float16 *)a.x + (uint64_t)xrow * a.ldx;
@@ -914,7 +925,7 @@ __device__ __forceinline__ void gemv_mfma_xr(const VkfGemvArgs &a, unsigned char
             }
         }
         // the next round's weights load under the reduction
-        if (tile + gridDim.x < ntiles && ng > 0) load_round(tile + gridDim.x, cur);
+        if (tile + tstep() < ntiles && ng > 0) load_round(tile + tstep(), cur);
         *(vkf_f4 *)(red + (wave * 64 + lane) * 4) = y4;
         __syncthreads();
         if (wave == 0) {
@@ -929,30 +940,51 @@ __device__ __forceinline__ void gemv_mfma_xr(const VkfGemvArgs &a, unsigned char
             for (int e = 0; e < 4; e++) {
                 const uint32_t m = 4 * lg + e;
                 if (m < a.M && n < a.N) {
-                    float *yp = a.y + (uint64_t)m * a.ldy + n;
-                    *yp = (a.flags & 1u) ? *yp + s[e] : s[e];
+                    if constexpr (KS) {
+                        a.y[((uint64_t)slice * a.M + m) * a.ldy + n] = s[e];
+                    } else {
+                        float *yp = a.y + (uint64_t)m * a.ldy + n;
+                        *yp = (a.flags & 1u) ? *yp + s[e] : s[e];
+                    }
                 }
             }
         }
         __syncthreads();
     };
-    uint32_t tile = blockIdx.x;
+    uint32_t tile = KS ? blockIdx.x / S : blockIdx.x;
     if (tile < ntiles && ng > 0) load_round(tile, ta);
-    for (; tile < ntiles; tile += gridDim.x) round(tile, ta);  // workgroup-uniform
+    for (; tile < ntiles; tile += tstep()) round(tile, ta);  // workgroup-uniform
 }
 
-template <int F, int NG, int P>
+template <int F, int NG, int P, bool KS>
 __device__ __forceinline__ void gemv_mfma_xr_entry(const VkfGemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    if (a.M <= 4) gemv_mfma_xr<F, 4, NG, P>(a, smem);
-    else if (a.M <= 8) gemv_mfma_xr<F, 8, NG, P>(a, smem);
-    else gemv_mfma_xr<F, 16, NG, P>(a, smem);
+    if (a.M <= 4) gemv_mfma_xr<F, 4, NG, P, KS>(a, smem);
+    else if (a.M <= 8) gemv_mfma_xr<F, 8, NG, P, KS>(a, smem);
+    else gemv_mfma_xr<F, 16, NG, P, KS>(a, smem);
 }
-// vkf_gemv_mfma_xr_<q>_f16_p<P>: P waves, up to NG = ceil(G / P) groups each
+// vkf_gemv_mfma_xr_<q>_f16_p<P>: P waves, up to NG = ceil(G / P) groups each;
+// vkf_gemv_mfma_xr_<q>_f16_p<P>_ks: the same on K slices of up to NG*P groups
 #define VKF_GEMV_MFMA_XR(name, F, NG, P)                                                                   \
     VKF_KERNEL void __launch_bounds__(64 * P) vkf_gemv_mfma_xr_##name##_f16_p##P(VkfGemvArgs a) {        \
-        gemv_mfma_xr_entry<F, NG, P>(a);                                                                 \
+        gemv_mfma_xr_entry<F, NG, P, false>(a);                                                          \
+    }                                                                                                    \
+    VKF_KERNEL void __launch_bounds__(64 * P) vkf_gemv_mfma_xr_##name##_f16_p##P##_ks(VkfGemvArgs a) {   \
+        gemv_mfma_xr_entry<F, NG, P, true>(a);                                                           \
     }
 VKF_GEMV_MFMA_XR(q4_0, GF_Q4_0, 1, 16)
 VKF_GEMV_MFMA_XR(q4_1, GF_Q4_1, 1, 16)
 VKF_GEMV_MFMA_XR(q4_k, GF_Q4_K, 2, 10)
+
+// y[m, n] = sum over s = 0, 1, ..., S-1 (in that order) of
+// part[(s*M + m)*N + n]: the K slices of vkf_gemv_mfma_xr_*_ks.  One thread
+// per output, grid (ceil(N / 256), M).
+VKF_KERNEL void __launch_bounds__(256) vkf_gemv_split_sum(VkfSplitSumArgs a) {
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+    if (n >= a.N || m >= a.M) return;
+    const uint64_t plane = (uint64_t)a.M * a.N;
+    const float *p = a.part + (uint64_t)m * a.N + n;
+    float s = p[0];
+    for (uint32_t k = 1; k < a.S; k++) s += p[k * plane];
+    a.y[(uint64_t)m * a.ldy + n] = s;
+}

@@ -51,9 +51,12 @@ def quantize_q8_1(x: torch.Tensor) -> torch.Tensor:
 def gemm_q(w: torch.Tensor, qtype: int, x: torch.Tensor, N: int, K: int, M: int | None = None,
            out: torch.Tensor | None = None, workspace: bool = True) -> torch.Tensor:
     """y[M, N] fp32 = x[M, K] @ deq(w)[N, K]^T.  x: fp16 / fp32 [M, K] or
-    uint8 Q8_1 rows [M, K/32*36].  Q8_1 activations at M > 16 get a torch
-    workspace for their one-time fp16 decode (vkflame_dispatch_gemm_q_ws);
-    workspace=False makes the GEMM decode them per tile instead."""
+    uint8 Q8_1 rows [M, K/32*36].  The routes that take a workspace get a
+    torch one (vkflame_dispatch_gemm_q_ws): Q8_1 activations at M > 16 for
+    their one-time fp16 decode, and the long-K matrix-core GEMV (Q4_K, Q4_0,
+    Q4_1 at 2 <= M <= 16) for its K-slice partials; workspace=False runs
+    their no-workspace forms (activation tiles decoded per GEMM tile, K
+    slices one launch after another)."""
     if x.dtype == torch.float16:
         xd, ldx = L.DTYPE_FP16, x.stride(0)
     elif x.dtype == torch.float32:
@@ -65,7 +68,7 @@ def gemm_q(w: torch.Tensor, qtype: int, x: torch.Tensor, N: int, K: int, M: int 
     M = x.shape[0] if M is None else M
     y = torch.empty((M, N), dtype=torch.float32, device=x.device) if out is None else out
     row_bytes = w.stride(0) if w.dim() == 2 else 0
-    nws = lib().vkflame_gemm_q_workspace_bytes(xd, M, K) if workspace else 0
+    nws = lib().vkflame_gemm_q_workspace_bytes(qtype, xd, M, N, K) if workspace else 0
     ws = torch.empty(nws, dtype=torch.uint8, device=x.device) if nws else None
     check(lib().vkflame_dispatch_gemm_q_ws(_p(w), qtype, row_bytes, _p(x), xd, ldx, _p(y), y.stride(0), M, N, K,
                                            _p(ws), nws, _stream()), "gemm_q")
