@@ -977,14 +977,20 @@ VKF_GEMV_MFMA_XR(q4_1, GF_Q4_1, 1, 16)
 VKF_GEMV_MFMA_XR(q4_k, GF_Q4_K, 2, 10)
 
 // y[m, n] = sum over s = 0, 1, ..., S-1 (in that order) of
-// part[(s*M + m)*N + n]: the K slices of vkf_gemv_mfma_xr_*_ks.  One thread
-// per output, grid (ceil(N / 256), M).
+// part[(s*M + m)*N + n]: the K slices of vkf_gemv_mfma_xr_*_ks, S <= 8.  One
+// thread per output, grid (ceil(N / 256), M); the S loads are issued
+// together, then added in slice order.
 VKF_KERNEL void __launch_bounds__(256) vkf_gemv_split_sum(VkfSplitSumArgs a) {
     const uint32_t n = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
     if (n >= a.N || m >= a.M) return;
     const uint64_t plane = (uint64_t)a.M * a.N;
     const float *p = a.part + (uint64_t)m * a.N + n;
-    float s = p[0];
-    for (uint32_t k = 1; k < a.S; k++) s += p[k * plane];
+    float v[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8; k++) v[k] = k < a.S ? p[k * plane] : 0.0f;
+    float s = v[0];
+#pragma unroll
+    for (uint32_t k = 1; k < 8; k++)
+        if (k < a.S) s += v[k];
     a.y[(uint64_t)m * a.ldy + n] = s;
 }
