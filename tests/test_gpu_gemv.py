@@ -441,14 +441,16 @@ def test_gemv_mfma_q6_k_extreme_scales(dev):
     assert _per_row_err(y, x64, w, O.Q6_K, N, K) <= TOL_F32
 
 
-@pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_1, O.Q4_K, O.Q5_K], ids=["q4_0", "q4_1", "q4_k", "q5_k"])
+@pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_1, O.Q4_K, O.Q5_K, O.Q8_0], ids=["q4_0", "q4_1", "q4_k", "q5_k", "q8_0"])
 @pytest.mark.parametrize("kind", ["f16", "f32", "q8_1"])
 @pytest.mark.parametrize("NK", [(77, 1600), (77, 1664), (77, 1728), (3001, 4096), (100003, 2624)],
                          ids=["77x1600", "77x1664", "77x1728", "3001x4096", "100003x2624"])
 def test_gemv_dot_lds_tails(dev, qt, kind, NK):
     """M = 1 through LDS: row regions that end 4, 8 or 12 bytes into a
-    16-byte piece (Q4_0 / Q4_1 rows of 25..27 chunks; on the large N in the
-    middle of a multi-iteration row walk), checked on a spread of rows."""
+    16-byte piece (Q4_0 / Q4_1 / Q8_0 rows of 25..27 chunks; on the large N
+    in the middle of a multi-iteration row walk), checked on a spread of
+    rows.  Q8_0 runs on the twelve-wave variant (fp16 / fp32 activations;
+    Q8_1 ones take the register-loading kernel)."""
     from vkflame_amd import ops
     N, K = NK
     if qt in (O.Q4_K, O.Q5_K) and K % 256:

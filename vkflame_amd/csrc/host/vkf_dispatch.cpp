@@ -91,6 +91,9 @@ constexpr size_t kDotLdsM1 = 8 * 4096 + 4096, kDotLdsM4 = 4 * (8 * 4096 + 4096);
 constexpr int kDotMaxK = 256 * 64;
 // M = 1 through LDS: the activations plus two 3 KiB weight buffers per wave
 constexpr size_t kDotLdsL = kDotLdsM1 + 16 * 2 * 3 * 1024;
+// Q8_0 through LDS: 12 waves, two 5 KiB buffers each (kernels/gemv_dot.hip)
+constexpr int kDotQ8Waves = 12;
+constexpr size_t kDotLdsLQ8 = kDotLdsM1 + kDotQ8Waves * 2 * 5 * 1024;
 // kernels/gemv_q6k.hip, one activation row: x planes + two weight buffers
 // for each of its 8 waves
 constexpr size_t kDotLdsQ6 = 11 * 4096 + 8 * 2 * 7 * 1024;
@@ -343,6 +346,16 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
             static_assert(VKF_K_GEMV_DOTL_Q5_K_Q81 == VKF_K_GEMV_DOTL_Q4_0_F16 + 11, "dot GEMV table order");
             const VkfKernelId k = (VkfKernelId)(VKF_K_GEMV_DOTL_Q4_0_F16 + 3 * li + xk);
             return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * kDotWaves), a, S(stream), kDotLdsL);
+        }
+        // M = 1, Q8_0 x fp16 / fp32: the same through LDS on twelve waves
+        if (qt == VKF_Q8_0 && xk != 2 && M == 1 && (K % 64) == 0 && K <= kDotMaxK && kDotLdsLQ8 <= vkf::max_lds() &&
+            aligned(w, 4) && (row_bytes % 4) == 0) {
+            const uint32_t cus = (uint32_t)vkf::cu_count();
+            const uint32_t seg = dot_segment((uint32_t)N, (uint32_t)(K / 64), 1, cus * kDotQ8Waves);
+            const uint32_t tiles = cdiv(N, 64 / seg);
+            a.flags |= seg << 8;
+            return vkf::launch(xk == 0 ? VKF_K_GEMV_DOTL_Q8_0_F16 : VKF_K_GEMV_DOTL_Q8_0_F32,
+                               dim3(tiles < cus ? tiles : cus), dim3(64 * kDotQ8Waves), a, S(stream), kDotLdsLQ8);
         }
         const size_t lds = M == 1 ? kDotLdsM1 : kDotLdsM4;
         if (fi >= 0 && M <= 4 && (xk != 2 || (qt == VKF_Q8_0 && M == 1)) && (K % 64) == 0 && K <= kDotMaxK &&

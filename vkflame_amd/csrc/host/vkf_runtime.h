@@ -70,6 +70,8 @@
     X(GEMV_DOTL_Q5_K_F16, "vkf_gemv_dotl_q5_k_f16")        \
     X(GEMV_DOTL_Q5_K_F32, "vkf_gemv_dotl_q5_k_f32")        \
     X(GEMV_DOTL_Q5_K_Q81, "vkf_gemv_dotl_q5_k_q8_1")       \
+    X(GEMV_DOTL_Q8_0_F16, "vkf_gemv_dotl_q8_0_f16")        \
+    X(GEMV_DOTL_Q8_0_F32, "vkf_gemv_dotl_q8_0_f32")        \
     X(GEMV_MFMA_Q4_K_F16, "vkf_gemv_mfma_q4_k_f16")        \
     X(GEMV_MFMA_Q4_0_F16, "vkf_gemv_mfma_q4_0_f16")        \
     X(GEMV_MFMA_Q4_1_F16, "vkf_gemv_mfma_q4_1_f16")        \

@@ -494,8 +494,8 @@ __device__ __forceinline__ void gemv_dot(const VkfGemvArgs &a) {
 }
 
 // ---------------------------------------------------------------------------
-// M = 1 with the weights through LDS (Q4_0, Q4_1, Q4_K: 36- or 40-byte
-// chunks).  Per iteration a wave needs S consecutive chunks of each of its
+// M = 1 with the weights through LDS (Q4_0, Q4_1, Q4_K, Q5_K, Q8_0: 36-,
+// 40-, 44- or 68-byte chunks).  Per iteration a wave needs S consecutive chunks of each of its
 // 64/S rows: CB*S contiguous bytes per row, 4*CB 16-byte pieces per wave.
 // They are fetched with direct-to-LDS loads over consecutive addresses into
 // one of the wave's two LDS buffers (each 128-byte line requested once; a
@@ -504,16 +504,21 @@ __device__ __forceinline__ void gemv_dot(const VkfGemvArgs &a) {
 // iteration's loads fill the other buffer.  The last iteration's region may
 // end 4, 8 or 12 bytes into a piece: that piece is fetched shifted and its
 // valid bytes are loaded again into registers and written over it.
-// Dynamic LDS: dot_lds_bytes<1>() + DOT_WAVES * 2 * DOT_WBUF.
+// NWV waves per workgroup, NLD direct loads per lane per iteration (NLD * 64
+// >= 4 * CB pieces, more than 64 * (NLD - 1) so that every load instruction
+// has active lanes and the vmcnt waits count NLD per iteration).
+// Dynamic LDS: dot_lds_bytes<1>() + NWV * 2 * NLD * 1024.
 // ---------------------------------------------------------------------------
-template <int QT> constexpr uint32_t dot_cb() { return QT == VKF_Q4_1 ? 40 : QT == VKF_Q5_K ? 44 : 36; }
-#define DOT_NLD 3  // direct loads per lane per iteration (3 x 64 >= 4 * 44)
-#define DOT_WBUF (DOT_NLD * 64 * 16)
+template <int QT> constexpr uint32_t dot_cb() {
+    return QT == VKF_Q4_1 ? 40 : QT == VKF_Q5_K ? 44 : QT == VKF_Q8_0 ? 68 : 36;
+}
+#define DOT_NLD 3  // direct loads per lane per iteration (3 x 64 >= 4 * 44, > 2 x 64 >= 4 * 36)
 
-template <int QT, int XK, uint32_t S>
+template <int QT, int XK, uint32_t S, int NWV, int NLD>
 __device__ __forceinline__ void gemv_dot_lds(const VkfGemvArgs &a, unsigned char *smem) {
     using F = DotFmt<QT>;
     constexpr uint32_t CB = dot_cb<QT>(), TR = 64 / S, PR = CB * S / 16, NP = TR * PR;
+    static_assert(NP <= 64 * NLD && NP > 64 * (NLD - 1), "every direct load instruction has active lanes");
     const uint32_t C = a.K / 64;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -521,8 +526,9 @@ __device__ __forceinline__ void gemv_dot_lds(const VkfGemvArgs &a, unsigned char
     const uint32_t ntiles = (a.N + TR - 1) / TR;
     const uint32_t iters = (C + S - 1) / S;
     const uint32_t il = p & 3;  // Q4_K: chunk c = p + S*it has c & 3 == p & 3 (S % 4 == 0)
-    const uint32_t tstep = gridDim.x * DOT_WAVES;
-    unsigned char *wb = smem + dot_lds_bytes<1>() + wave * 2 * DOT_WBUF;
+    constexpr uint32_t WBUF = NLD * 64 * 16;
+    const uint32_t tstep = gridDim.x * NWV;
+    unsigned char *wb = smem + dot_lds_bytes<1>() + wave * 2 * WBUF;
     const uint32_t last = (uint32_t)a.row_bytes - 16;  // last 16-byte piece of a row (row_bytes % 4 == 0)
     const uint32_t rl = CB * S * (iters - 1), tl = (uint32_t)a.row_bytes - rl, rem = tl % 16;
     const bool straddle = rem != 0 && tl < 16 * PR;  // uniform
@@ -531,13 +537,13 @@ __device__ __forceinline__ void gemv_dot_lds(const VkfGemvArgs &a, unsigned char
     uint32_t fixp = 0xffffffffu, fixv[3] = {0, 0, 0};
     auto issue = [&](uint32_t it) {
         const uint32_t r0 = CB * S * it;  // region start within the row
-        unsigned char *buf = wb + (it & 1) * DOT_WBUF;
+        unsigned char *buf = wb + (it & 1) * WBUF;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the buffer are done
         // raised issue priority while the wave requests its next region: the
         // loads go out ahead of other waves' dot math (2 % at 13824x5120)
         __builtin_amdgcn_s_setprio(2);
 #pragma unroll
-        for (int j = 0; j < DOT_NLD; j++) {
+        for (int j = 0; j < NLD; j++) {
             const uint32_t P = 64 * j + lane, pp = P < NP ? P : NP - 1, rr = pp / PR;
             const uint32_t nn = tile * TR + rr < a.N ? tile * TR + rr : a.N - 1;
             const uint32_t off = r0 + 16 * (pp - rr * PR);
@@ -550,7 +556,7 @@ __device__ __forceinline__ void gemv_dot_lds(const VkfGemvArgs &a, unsigned char
             const uint8_t *fa = a.w;  // a valid address for lanes without one
             fixp = 0xffffffffu;
 #pragma unroll
-            for (int j = 0; j < DOT_NLD; j++) {
+            for (int j = 0; j < NLD; j++) {
                 const uint32_t P = 64 * j + lane, rr = P / PR;
                 if (rr < TR && P - rr * PR == tl / 16) {
                     const uint32_t nn = tile * TR + rr < a.N ? tile * TR + rr : a.N - 1;
@@ -584,12 +590,12 @@ __device__ __forceinline__ void gemv_dot_lds(const VkfGemvArgs &a, unsigned char
         for (uint32_t it = 0; it < iters; it++) {
             if (it + 1 < iters) {  // wave-uniform
                 issue(it + 1);
-                if (it + 2 == iters && straddle) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DOT_NLD + 3) : "memory");
-                else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DOT_NLD) : "memory");
+                if (it + 2 == iters && straddle) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD + 3) : "memory");
+                else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD) : "memory");
             } else {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             }
-            unsigned char *buf = wb + (it & 1) * DOT_WBUF;
+            unsigned char *buf = wb + (it & 1) * WBUF;
             if (it == iters - 1 && straddle && fixp != 0xffffffffu) {
 #pragma unroll
                 for (int d = 0; d < 3; d++)
@@ -626,14 +632,14 @@ __device__ __forceinline__ void gemv_dot_lds(const VkfGemvArgs &a, unsigned char
     }
 }
 
-template <int QT, int XK>
+template <int QT, int XK, int NWV = DOT_WAVES, int NLD = DOT_NLD>
 __device__ __forceinline__ void gemv_dot_lds_entry(const VkfGemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     switch ((a.flags >> 8) & 0xffu) {
-    case 8: gemv_dot_lds<QT, XK, 8>(a, smem); break;
-    case 16: gemv_dot_lds<QT, XK, 16>(a, smem); break;
-    case 32: gemv_dot_lds<QT, XK, 32>(a, smem); break;
-    default: gemv_dot_lds<QT, XK, 64>(a, smem); break;
+    case 8: gemv_dot_lds<QT, XK, 8, NWV, NLD>(a, smem); break;
+    case 16: gemv_dot_lds<QT, XK, 16, NWV, NLD>(a, smem); break;
+    case 32: gemv_dot_lds<QT, XK, 32, NWV, NLD>(a, smem); break;
+    default: gemv_dot_lds<QT, XK, 64, NWV, NLD>(a, smem); break;
     }
 }
 
@@ -681,3 +687,15 @@ VKF_GEMV_DOTL(q4_0, VKF_Q4_0)
 VKF_GEMV_DOTL(q4_1, VKF_Q4_1)
 VKF_GEMV_DOTL(q4_k, VKF_Q4_K)
 VKF_GEMV_DOTL(q5_k, VKF_Q5_K)
+// Q8_0 (68-byte chunks, 4352 bytes per wave and iteration: five direct loads
+// per lane) on twelve waves, whose two buffers each fit LDS beside the
+// activations (dot_lds_bytes<1>() + 12 * 2 * 5 KiB = 156 KiB):
+// vkf_gemv_dotl_q8_0_{f16,f32}
+#define DOT_Q8_WAVES 12
+#define DOT_Q8_NLD 5
+VKF_KERNEL void __launch_bounds__(64 * DOT_Q8_WAVES) vkf_gemv_dotl_q8_0_f16(VkfGemvArgs a) {
+    gemv_dot_lds_entry<VKF_Q8_0, 0, DOT_Q8_WAVES, DOT_Q8_NLD>(a);
+}
+VKF_KERNEL void __launch_bounds__(64 * DOT_Q8_WAVES) vkf_gemv_dotl_q8_0_f32(VkfGemvArgs a) {
+    gemv_dot_lds_entry<VKF_Q8_0, 1, DOT_Q8_WAVES, DOT_Q8_NLD>(a);
+}
