@@ -132,8 +132,9 @@ int vkflame_dispatch_gemm_q(const void *w, int quant_type, uint64_t row_bytes, c
  *    fp16-activation GEMM runs on them (from M = 256 with 256-row tiles);
  *    without it the GEMM decodes activation tiles itself.  Both multiply the
  *    same fp16 operand values.
- *  - Q4_K (K > 5120) and Q4_0 / Q4_1 (K > 4096) weights, fp16 activations,
- *    2 <= M <= 16, at most 8 K slices (of 20 / 16 256-k groups): S*M*N*4
+ *  - Q4_K (K > 5120) and Q4_0 / Q4_1 (K > 4096) weights at 2 <= M <= 16,
+ *    Q8_0 (K > 6144) at 9 <= M <= 16, fp16 activations, at most 8 K slices
+ *    (of 20 / 16 / 24 256-k groups): S*M*N*4
  *    bytes hold the partial products of S K slices, which run side by side
  *    on the matrix-core GEMV and are added in slice order by a second
  *    launch; without it the slices run one launch after another.

@@ -211,6 +211,9 @@ def test_c_abi_rejects_bad_arguments():
     assert ws(q6k, VL.DTYPE_FP16, 8, 5120, 13824) == 0
     assert ws(q4k, VL.DTYPE_FP16, 8, 5120, 256 * 161) == 0  # more than 8 slices
     assert ws(q4k, VL.DTYPE_FP16, 8, 5120, 256 * 160) == 8 * 8 * 5120 * 4
+    q8_0 = 2  # VKF_DEQUANT_Q8_0
+    assert ws(q8_0, VL.DTYPE_FP16, 16, 5120, 13824) == 3 * 16 * 5120 * 4  # Q8_0: 24-group slices at M > 8
+    assert ws(q8_0, VL.DTYPE_FP16, 8, 5120, 13824) == 0 and ws(q8_0, VL.DTYPE_FP16, 16, 5120, 6144) == 0
     qws = L.vkflame_dispatch_gemm_q_ws
     assert qws(P(16), 4, 0, P(16), 1, 0, P(16), 0, 1, 8, 300, None, 0, s) == 1     # K % 256
     assert qws(P(16), 6, 0, P(18), 11, 0, P(16), 0, 64, 8, 256, P(16), 1 << 20, s) == 1  # Q8_1 x not 4-aligned

@@ -296,22 +296,23 @@ def test_gemv_mfma_many_rounds(dev, qt, K, M):
     assert _per_row_err(y, x64, w, qt, N, K) <= TOL_F32
 
 
-KS_CASES = [(O.Q4_K, 256 * 34), (O.Q4_K, 13824), (O.Q4_K, 256 * 160), (O.Q4_0, 256 * 36), (O.Q4_0, 11008),
-            (O.Q4_1, 11008), (O.Q4_1, 256 * 128)]
+KS_CASES = [(q, k, m) for q, k in [(O.Q4_K, 256 * 34), (O.Q4_K, 13824), (O.Q4_K, 256 * 160), (O.Q4_0, 256 * 36),
+                                    (O.Q4_0, 11008), (O.Q4_1, 11008), (O.Q4_1, 256 * 128)] for m in (2, 7, 16)]
+KS_CASES += [(O.Q8_0, 13824, 9), (O.Q8_0, 13824, 16), (O.Q8_0, 256 * 192, 16)]
 
 
-@pytest.mark.parametrize("qt,K", KS_CASES, ids=[f"{O.QNAMES[q]}-{k}" for q, k in KS_CASES])
-@pytest.mark.parametrize("M", [2, 7, 16])
+@pytest.mark.parametrize("qt,K,M", KS_CASES, ids=[f"{O.QNAMES[q]}-{k}-m{m}" for q, k, m in KS_CASES])
 @pytest.mark.parametrize("N", [77, "rounds"])
 def test_gemv_mfma_k_slices(dev, qt, K, M, N):
     """Long K on the register-activation kernel as K slices side by side in
     one launch (2 to 8 slices: K/256 = 34 and 36 groups, 13824, 11008, and
-    the longest K the route takes, 8 slices of 20 or 16 groups), each
-    workgroup on one slice, the partials added in slice order by a second
-    launch: against the float64 product per activation row, against the
-    no-workspace route (K-slice launches one after another) within the same
-    tolerance, and bit for bit between two calls.  N = "rounds" gives every
-    workgroup more than one 16-row tile and a ragged last tile."""
+    the longest K the route takes, 8 slices of 20, 16 or 24 groups; Q8_0 at
+    M > 8 only), each workgroup on one slice, the partials added in slice
+    order by a second launch: against the float64 product per activation
+    row, against the no-workspace route (K-slice launches one after another)
+    within the same tolerance, and bit for bit between two calls.  N =
+    "rounds" gives every workgroup more than one 16-row tile and a ragged
+    last tile."""
     import torch
     from vkflame_amd import ops
     from vkflame_amd import _lib as L

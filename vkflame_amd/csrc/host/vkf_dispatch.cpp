@@ -62,10 +62,11 @@ VkfKernelId gemm_kernel(int qt, int xk) {
 // chunk loads need the row starts aligned as below (36-, 40-, 68-, 144- and
 // 176-byte chunk groups).
 // K-sliced register-activation GEMV (kernels/gemv_mfma.hip gemv_mfma_xr, KS):
-// Q4_K (ten waves of two 256-k groups) and Q4_0 / Q4_1 (sixteen waves of
-// one) with fp16 activations, 2 <= M <= 16, on up to kMaxKSlices slices, at
-// a K too long for one workgroup's waves to hold (Q4_K above 5120, Q4_0 /
-// Q4_1 above 4096) whose activation image does not fit one launch of the
+// Q4_K (ten waves of two 256-k groups), Q4_0 / Q4_1 (sixteen waves of one)
+// and, at 9 <= M <= 16, Q8_0 (twelve waves of two) with fp16 activations,
+// 2 <= M <= 16, on up to kMaxKSlices slices, at a K too long for one
+// workgroup's waves to hold (Q4_K above 5120, Q4_0 / Q4_1 above 4096, Q8_0
+// above 6144) whose activation image does not fit one launch of the
 // LDS-image kernel either (160 KiB of LDS on gfx950; 5120x5376 Q4_K M = 8:
 // 11.5 us in one LDS-image launch, 13.6 us on two K slices; 5120x13824
 // M = 8 / 16: 27.9 / 44.4 us in two LDS-image launches, 17.5 / 18.6 us on
@@ -75,7 +76,10 @@ constexpr uint32_t kMaxKSlices = 8;
 constexpr size_t kLdsGfx950 = 160 * 1024;
 uint32_t ks_slices(int qt, int x_dtype, int M, int K) {
     if (x_dtype != VKF_DTYPE_FP16 || M < 2 || M > 16 || K <= 0 || (K % 256) != 0) return 0;
-    const uint32_t per = qt == VKF_Q4_K ? 20 : (qt == VKF_Q4_0 || qt == VKF_Q4_1) ? 16 : 0;
+    const uint32_t per = qt == VKF_Q4_K                     ? 20
+                         : (qt == VKF_Q4_0 || qt == VKF_Q4_1) ? 16
+                         : (qt == VKF_Q8_0 && M > 8)          ? 24
+                                                              : 0;
     const uint32_t nsb = (uint32_t)(K / 256);
     const size_t per_group = (size_t)(M <= 8 ? 8 : 16) * (qt == VKF_Q4_K ? 544 : 512);  // LDS image, 256 k
     if (per == 0 || nsb <= per || nsb <= (kLdsGfx950 - kMfmaRed) / per_group) return 0;
@@ -290,16 +294,26 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
                                           : mf == 1 ? VKF_K_GEMV_MFMA_XR_Q4_0_F16 : VKF_K_GEMV_MFMA_XR_Q4_1_F16;
                 return vkf::launch(k, dim3(tiles < cus ? tiles : cus), dim3(64 * P), a, S(stream), 1024 * P);
             }
+            // Q8_0 at 9 <= M <= 16 with K <= 6144 on 12 waves of two groups
+            // (13824x5120 M = 16 30.7 -> 25.9 us; at M <= 8 the LDS-image
+            // kernel stays ahead, 20.2 against 25.2 us at M = 8)
+            if (xk == 0 && mf == 5 && M > 8 && K <= 6144) {
+                const uint32_t tiles = cdiv(N, 16), cus = (uint32_t)vkf::cu_count(), P = 12;
+                return vkf::launch(VKF_K_GEMV_MFMA_XR_Q8_0_F16_P12, dim3(tiles < cus ? tiles : cus), dim3(64 * P), a,
+                                   S(stream), 1024 * P);
+            }
             // longer K on K slices, one slice per workgroup, the partials in
             // the workspace summed in slice order by a second launch
             const uint32_t ns = xk == 0 ? ks_slices(qt, x_dtype, M, K) : 0;
             if (ns && workspace && aligned(workspace, 16) &&
                 workspace_bytes >= vkflame_gemm_q_workspace_bytes(qt, x_dtype, M, N, K)) {
-                const uint32_t tiles = cdiv(N, 16), cus = (uint32_t)vkf::cu_count(), P = mf == 0 ? 10 : 16;
+                const uint32_t tiles = cdiv(N, 16), cus = (uint32_t)vkf::cu_count();
+                const uint32_t P = mf == 0 ? 10 : mf == 5 ? 12 : 16;
                 const uint32_t lanes = cus / ns == 0 ? 1 : (tiles < cus / ns ? tiles : cus / ns);
                 const VkfKernelId k = mf == 0   ? VKF_K_GEMV_MFMA_XR_Q4_K_F16_P10_KS
                                       : mf == 1 ? VKF_K_GEMV_MFMA_XR_Q4_0_F16_KS
-                                                : VKF_K_GEMV_MFMA_XR_Q4_1_F16_KS;
+                                      : mf == 2 ? VKF_K_GEMV_MFMA_XR_Q4_1_F16_KS
+                                                : VKF_K_GEMV_MFMA_XR_Q8_0_F16_P12_KS;
                 VkfGemvArgs b = a;
                 b.y = (float *)workspace;
                 b.ldy = (uint64_t)N;

@@ -137,6 +137,8 @@
     X(GEMV_MFMA_XR_Q4_1_F16_KS, "vkf_gemv_mfma_xr_q4_1_f16_p16_ks") \
     X(GEMV_MFMA_XR_Q4_K_F16_P10_KS, "vkf_gemv_mfma_xr_q4_k_f16_p10_ks") \
     X(GEMV_SPLIT_SUM, "vkf_gemv_split_sum")                 \
+    X(GEMV_MFMA_XR_Q8_0_F16_P12, "vkf_gemv_mfma_xr_q8_0_f16_p12") \
+    X(GEMV_MFMA_XR_Q8_0_F16_P12_KS, "vkf_gemv_mfma_xr_q8_0_f16_p12_ks") \
     X(GEMM_F16_SKINNY, "vkf_gemm_f16_skinny")               \
     /* GEMM: fp16 and Q8_1 activations per weight type */   \
     X(GEMM_Q4_0_F16, "vkf_gemm_q4_0_f16")                   \

@@ -975,6 +975,7 @@ __device__ __forceinline__ void gemv_mfma_xr_entry(const VkfGemvArgs &a) {
 VKF_GEMV_MFMA_XR(q4_0, GF_Q4_0, 1, 16)
 VKF_GEMV_MFMA_XR(q4_1, GF_Q4_1, 1, 16)
 VKF_GEMV_MFMA_XR(q4_k, GF_Q4_K, 2, 10)
+VKF_GEMV_MFMA_XR(q8_0, GF_Q8_0, 2, 12)
 
 // y[m, n] = sum over s = 0, 1, ..., S-1 (in that order) of
 // part[(s*M + m)*N + n]: the K slices of vkf_gemv_mfma_xr_*_ks, S <= 8.  One

@@ -54,9 +54,9 @@ def gemm_q(w: torch.Tensor, qtype: int, x: torch.Tensor, N: int, K: int, M: int 
     uint8 Q8_1 rows [M, K/32*36].  The routes that take a workspace get a
     torch one (vkflame_dispatch_gemm_q_ws): Q8_1 activations at M > 16 for
     their one-time fp16 decode, and the long-K matrix-core GEMV (Q4_K, Q4_0,
-    Q4_1 at 2 <= M <= 16) for its K-slice partials; workspace=False runs
-    their no-workspace forms (activation tiles decoded per GEMM tile, K
-    slices one launch after another)."""
+    Q4_1 at 2 <= M <= 16, Q8_0 at 9 <= M <= 16) for its K-slice partials;
+    workspace=False runs their no-workspace forms (activation tiles decoded
+    per GEMM tile, K slices one launch after another)."""
     if x.dtype == torch.float16:
         xd, ldx = L.DTYPE_FP16, x.stride(0)
     elif x.dtype == torch.float32:
