@@ -125,6 +125,9 @@
     X(GEMM_I8_N4, "vkf_gemm_i8_n4")                         \
     X(GEMM_I8_N5, "vkf_gemm_i8_n5")                         \
     X(GEMM_F16_N4T, "vkf_gemm_f16_n4t")                     \
+    X(GEMM_F16_N2, "vkf_gemm_f16_n2")                       \
+    X(GEMM_I8_N2, "vkf_gemm_i8_n2")                         \
+    X(GEMM_F16_N2T, "vkf_gemm_f16_n2t")                     \
     X(GEMM_F16_N5T, "vkf_gemm_f16_n5t")                     \
     X(GEMM_F16_B256, "vkf_gemm_f16_b256")                   \
     X(GEMM_I8_B256, "vkf_gemm_i8_b256")                     \
@@ -220,9 +223,10 @@ void *real_hip_symbol(const char *name);
 // the library or symbol is absent.
 void *vendor_symbol(const char *lib, const char *name);
 
-// Tile width (16·nb columns) of the narrow-tile GEMMs for this grid, 0 if
-// they do not apply (es: bytes per X element).
-uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es);
+// Tile width (16·nb columns, nb in {2, 4, 5} from min_nb up) of the
+// narrow-tile GEMMs for this grid, 0 if they do not apply (es: bytes per X
+// element).
+uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es, uint32_t min_nb = 4);
 
 // Number of compute units of the current device (cached per device).
 int cu_count();
