@@ -181,32 +181,34 @@ def test_linear_dense_split_k_and_plain(dev):
         assert rel_err(D.cpu().numpy(), ref) <= TOL_F32, (M, N, K)
 
 
-def _narrow_nb(M, N, K, es, cus, batch=1, min_nb=4):
+def _narrow_nb(M, N, K, es, cus, batch=1, nbs=(4, 5)):
     """The tile width the host picks for the narrow-tile kernels (16*nb
-    columns; the dense kernels from nb = 2, the Q4_K one from 4), 0 if it
-    takes another kernel (mirrors narrow_nb in csrc/host/vkf_runtime.cpp)."""
+    columns; the dense NT kernels nb = 1..5, NN 1, 2, 4, 5, the Q4_K one 4
+    and 5), 0 if it takes another kernel (mirrors narrow_nb in
+    csrc/host/vkf_runtime.cpp)."""
     rows = -(-M // 128) * batch
     if K == 0 or (K * es) % 256 or rows * -(-N // 128) >= cus:
         return 0
-    for nb in (2, 4, 5):
-        if nb >= min_nb and rows * -(-N // (16 * nb)) <= cus:
+    for nb in nbs:
+        if rows * -(-N // (16 * nb)) <= cus:
             return nb
     return 0
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 5120, 5120), (512, 4096, 1024), (500, 5000, 768), (128, 8192, 2048),
-                                   (77, 200, 256), (384, 3000, 512), (1024, 1024, 1024), (300, 1000, 512)])
+                                   (77, 200, 256), (384, 3000, 512), (1024, 1024, 1024), (300, 1000, 512), (128, 4096, 512),
+                                   (256, 5120, 512), (512, 3000, 256)])
 def test_linear_dense_narrow_tiles(dev, M, N, K):
     """Grids of fewer 128x128 tiles than CUs with whole pairs of K steps:
-    the narrow-tile kernels (128 x 32, 128 x 64 or 128 x 80 tiles, three
-    stages, K split between two wave groups).  int8 -> exact int32 (also
+    the narrow-tile kernels (128 x 16 to 128 x 80 tiles, three stages, K
+    split between two wave groups).  int8 -> exact int32 (also
     with integer alpha / beta), fp16 -> fp32 and fp16 with alpha, beta*C,
     bias-free activation; repeated calls give the same bits."""
     import torch
     from vkflame_amd import ops
     from vkflame_amd._lib import DTYPE_FP16, DTYPE_FP16_FP32OUT, DTYPE_INT8_INT32OUT
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    assert _narrow_nb(M, N, K, 1, cus, min_nb=2) in (2, 4, 5) and _narrow_nb(M, N, K, 2, cus, min_nb=2) in (2, 4, 5)
+    assert _narrow_nb(M, N, K, 1, cus, nbs=(1, 2, 3, 4, 5)) and _narrow_nb(M, N, K, 2, cus, nbs=(1, 2, 3, 4, 5))
     rng = np.random.default_rng(seed_for(4, 82) + M + N + K)
     A = rng.integers(-127, 128, (M, K)).astype(np.int8)
     W = rng.integers(-127, 128, (N, K)).astype(np.int8)
@@ -233,18 +235,19 @@ def test_linear_dense_narrow_tiles(dev, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 8192, 2048), (512, 4096, 1024), (300, 1000, 512), (77, 200, 256),
-                                   (512, 5120, 5120), (500, 5000, 768), (1024, 1024, 1024), (256, 256, 256)])
+                                   (512, 5120, 5120), (500, 5000, 768), (1024, 1024, 1024), (256, 256, 256), (128, 4096, 512),
+                                   (256, 5120, 512), (512, 3000, 256)])
 def test_linear_fp16_nn_narrow_tiles(dev, M, N, K):
     """fp16 with B stored [K, N] (NN) on grids of fewer 128x128 tiles than
-    CUs: the narrow kernel's 128 x 32, 128 x 64 or 128 x 80 tiles with B's
-    k-rows staged as they lie and read back transposed.  fp32 out against
+    CUs: the narrow kernel's 128 x 16 to 128 x 80 tiles with B's k-rows
+    staged as they lie and read back transposed.  fp32 out against
     the float64 product, repeatable bits, and fp16 out with alpha, beta*C
     and an activation."""
     import torch
     from vkflame_amd import ops
     from vkflame_amd._lib import DTYPE_FP16, DTYPE_FP16_FP32OUT
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    assert M > 64 and N % 8 == 0 and _narrow_nb(M, N, K, 2, cus, min_nb=2) in (2, 4, 5)
+    assert M > 64 and N % 8 == 0 and _narrow_nb(M, N, K, 2, cus, nbs=(1, 2, 4, 5))
     rng = np.random.default_rng(seed_for(4, 83) + M + N + K)
     A, B, C = _f16(rng, M, K), _f16(rng, K, N), _f16(rng, M, N)
     ref = A.astype(np.float64) @ B.astype(np.float64)

@@ -471,7 +471,7 @@ int vkflame_dispatch_gemm_q_ws(const void *w, int qt, uint64_t row_bytes, const 
     // nb·8 KiB, raw pieces nb·4.5 KiB)
     if (qt == VKF_Q4_K && xk == 0 && aligned(x, 16) && (ldx % 8) == 0 && (K % 256) == 0 && aligned(w, 16) &&
         (row_bytes % 16) == 0) {
-        const uint32_t nb = vkf::narrow_nb(g, 1, 2);
+        const uint32_t nb = vkf::narrow_nb(g, 1, 2, vkf::kNarrowQ4K);
         if (nb) {
             const size_t lds = 98304 + (size_t)nb * (4 * 2048 + 6 * 768);
             return vkf::launch(nb == 4 ? VKF_K_GEMM_Q4_K_F16_N4 : VKF_K_GEMM_Q4_K_F16_N5,

@@ -187,12 +187,12 @@ static bool skinny_ok(const VkfGemmArgs &g, uint32_t batch) {
 // (the least traffic per CU with the most CUs busy); 0 when neither fits
 // or the 128 x 128 grid already fills the CUs.
 constexpr uint32_t kNarrowStages = 3;
-uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es, uint32_t min_nb) {
+uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es, uint32_t nbs) {
     if (g.K == 0 || ((uint64_t)g.K * es) % 256 != 0) return 0;
     const uint64_t cus = (uint64_t)cu_count(), rows = ((uint64_t)g.R + 127) / 128 * batch;
     if (rows * (((uint64_t)g.Cn + 127) / 128) >= cus) return 0;
-    for (uint32_t nb : {2u, 4u, 5u})
-        if (nb >= min_nb && rows * (((uint64_t)g.Cn + 16 * nb - 1) / (16 * nb)) <= cus) return nb;
+    for (uint32_t nb = 1; nb <= 5; nb++)
+        if (((nbs >> nb) & 1u) && rows * (((uint64_t)g.Cn + 16 * nb - 1) / (16 * nb)) <= cus) return nb;
     return 0;
 }
 
@@ -214,12 +214,13 @@ hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream,
             dma_operand(g.Y, g.ldy, (g.flags & VKF_GF_Y_TRANS) != 0, g.K, es)) {
             // narrow tiles (128 x 16·nb) where they give the CUs more of the
             // grid: the narrowest whose grid still fits one tile per CU
-            const uint32_t nb = narrow_nb(g, batch, es, 2);
+            const uint32_t nb = narrow_nb(g, batch, es, kNarrowAll);
             if (nb) {
-                static const VkfKernelId nk[2][3] = {{VKF_K_GEMM_I8_N2, VKF_K_GEMM_I8_N4, VKF_K_GEMM_I8_N5},
-                                                     {VKF_K_GEMM_F16_N2, VKF_K_GEMM_F16_N4, VKF_K_GEMM_F16_N5}};
+                static const VkfKernelId nk[2][5] = {
+                    {VKF_K_GEMM_I8_N1, VKF_K_GEMM_I8_N2, VKF_K_GEMM_I8_N3, VKF_K_GEMM_I8_N4, VKF_K_GEMM_I8_N5},
+                    {VKF_K_GEMM_F16_N1, VKF_K_GEMM_F16_N2, VKF_K_GEMM_F16_N3, VKF_K_GEMM_F16_N4, VKF_K_GEMM_F16_N5}};
                 const dim3 gn((g.Cn + 16 * nb - 1) / (16 * nb), grid.y, batch);
-                return launch(nk[es - 1][nb == 2 ? 0 : nb - 3], gn, dim3(512), &g, sizeof(g), stream,
+                return launch(nk[es - 1][nb - 1], gn, dim3(512), &g, sizeof(g), stream,
                               kNarrowStages * 2 * (16384 + nb * 16 * 128));
             }
             return launch(id == VKF_K_GEMM_F16 ? VKF_K_GEMM_F16_K2 : VKF_K_GEMM_I8_K2, grid, dim3(512), &g,
@@ -230,9 +231,13 @@ hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream,
         if (id == VKF_K_GEMM_F16 && (g.flags & VKF_GF_Y_TRANS) &&
             dma_operand(g.X, g.ldx, (g.flags & VKF_GF_X_TRANS) != 0, g.K, 2) && (g.ldy * 2) % 16 == 0 &&
             ((uintptr_t)g.Y & 15) == 0 && g.Cn % 8 == 0) {
-            const uint32_t nb = narrow_nb(g, batch, 2, 2);
+            static const VkfKernelId nt[5] = {VKF_K_GEMM_F16_N1T, VKF_K_GEMM_F16_N2T, VKF_K_GEMM_F16_N4T,
+                                              VKF_K_GEMM_F16_N4T, VKF_K_GEMM_F16_N5T};  // nb = 3 not taken
+            // (not the 48-column tiles: 512x3072x1024 NN 12.9 us on 128 x 64,
+            // 13.6 on 128 x 48)
+            const uint32_t nb = narrow_nb(g, batch, 2, kNarrowAll & ~(1u << 3));
             if (nb)
-                return launch(nb == 2 ? VKF_K_GEMM_F16_N2T : nb == 4 ? VKF_K_GEMM_F16_N4T : VKF_K_GEMM_F16_N5T,
+                return launch(nt[nb - 1],
                               dim3((g.Cn + 16 * nb - 1) / (16 * nb), grid.y, batch), dim3(512), &g, sizeof(g), stream,
                               kNarrowStages * 2 * (16384 + nb * 16 * 128));
         }

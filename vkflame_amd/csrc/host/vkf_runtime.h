@@ -128,6 +128,11 @@
     X(GEMM_F16_N2, "vkf_gemm_f16_n2")                       \
     X(GEMM_I8_N2, "vkf_gemm_i8_n2")                         \
     X(GEMM_F16_N2T, "vkf_gemm_f16_n2t")                     \
+    X(GEMM_F16_N1, "vkf_gemm_f16_n1")                       \
+    X(GEMM_I8_N1, "vkf_gemm_i8_n1")                         \
+    X(GEMM_F16_N1T, "vkf_gemm_f16_n1t")                     \
+    X(GEMM_F16_N3, "vkf_gemm_f16_n3")                       \
+    X(GEMM_I8_N3, "vkf_gemm_i8_n3")                         \
     X(GEMM_F16_N5T, "vkf_gemm_f16_n5t")                     \
     X(GEMM_F16_B256, "vkf_gemm_f16_b256")                   \
     X(GEMM_I8_B256, "vkf_gemm_i8_b256")                     \
@@ -223,10 +228,12 @@ void *real_hip_symbol(const char *name);
 // the library or symbol is absent.
 void *vendor_symbol(const char *lib, const char *name);
 
-// Tile width (16·nb columns, nb in {2, 4, 5} from min_nb up) of the
-// narrow-tile GEMMs for this grid, 0 if they do not apply (es: bytes per X
-// element).
-uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es, uint32_t min_nb = 4);
+// Tile width (16·nb columns) of the narrow-tile GEMMs for this grid: the
+// narrowest of those allowed (bit nb of nbs) whose grid fits one tile per
+// CU, 0 if none does or they do not apply (es: bytes per X element).
+constexpr uint32_t kNarrowAll = 0x3e;                 // nb = 1 .. 5 (dense kernels)
+constexpr uint32_t kNarrowQ4K = (1u << 4) | (1u << 5);  // the Q4_K kernel's two widths
+uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es, uint32_t nbs);
 
 // Number of compute units of the current device (cached per device).
 int cu_count();

@@ -2259,7 +2259,7 @@ __device__ __forceinline__ void mfma_step_n(const uint8_t *lx, const uint8_t *ly
 // or 40 dwords apart already fall on different banks).
 template <int NB>
 __device__ __forceinline__ uint32_t trb_slot(uint32_t p, uint32_t k) {
-    static_assert(NB == 2 || NB == 4 || NB == 5, "NN narrow tiles: 32, 64 or 80 columns");
+    static_assert(NB >= 1 && NB <= 5, "NN narrow tiles: 16 to 80 columns");
     return NB == 4 ? p ^ (2 * (k & 3)) : p;
 }
 template <int NB, class ACC>
@@ -2536,14 +2536,22 @@ __device__ __forceinline__ void gemm_n_body(const VkfGemmArgs &a0, uint8_t *smem
         extern __shared__ __attribute__((aligned(16))) uint8_t gn_smem[];          \
         gemm_n_body<ES, NB, ACC>(a, gn_smem);                                        \
     }
+VKF_GEMM_N(f16, 2, vkf_f4, 1)
 VKF_GEMM_N(f16, 2, vkf_f4, 2)
+VKF_GEMM_N(f16, 2, vkf_f4, 3)
 VKF_GEMM_N(f16, 2, vkf_f4, 4)
 VKF_GEMM_N(f16, 2, vkf_f4, 5)
+VKF_GEMM_N(i8, 1, vkf_i4, 1)
 VKF_GEMM_N(i8, 1, vkf_i4, 2)
+VKF_GEMM_N(i8, 1, vkf_i4, 3)
 VKF_GEMM_N(i8, 1, vkf_i4, 4)
 VKF_GEMM_N(i8, 1, vkf_i4, 5)
-// fp16 with Y stored [K, C] (NN), 128 x 32, 128 x 64 or 128 x 80 tiles; Y:
-// 16-byte aligned, ldy % 8 == 0, C % 8 == 0
+// fp16 with Y stored [K, C] (NN), 128 x 16, 32, 64 or 80 tiles; Y: 16-byte
+// aligned, ldy % 8 == 0, C % 8 == 0
+VKF_KERNEL void __launch_bounds__(512) vkf_gemm_f16_n1t(VkfGemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t gn_smem[];
+    gemm_n_body<2, 1, vkf_f4, true>(a, gn_smem);
+}
 VKF_KERNEL void __launch_bounds__(512) vkf_gemm_f16_n2t(VkfGemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t gn_smem[];
     gemm_n_body<2, 2, vkf_f4, true>(a, gn_smem);
