@@ -181,11 +181,11 @@ static bool skinny_ok(const VkfGemmArgs &g, uint32_t batch) {
     return !(g.flags & VKF_GF_Y_TRANS) || g.Cn % 8 == 0;
 }
 
-// The narrow-tile kernels (vkf_gemm_{f16,i8,q4_k_f16}_n{4,5}, kernels/gemm.hip):
-// 128 x 16·nb tiles, three stages of both K groups' steps, whole pairs of
-// 128-byte K steps.  The narrowest tile whose grid fits one tile per CU
-// (the least traffic per CU with the most CUs busy); 0 when neither fits
-// or the 128 x 128 grid already fills the CUs.
+// The narrow-tile kernels (vkf_gemm_{f16,i8}_n{1..5}, vkf_gemm_q4_k_f16_n{4,5},
+// kernels/gemm.hip): 128 x 16·nb tiles, three stages of both K groups'
+// steps, whole pairs of 128-byte K steps.  The narrowest allowed tile whose
+// grid fits one tile per CU (the most CUs busy); 0 when none fits or the
+// 128 x 128 grid already fills the CUs.
 constexpr uint32_t kNarrowStages = 3;
 uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es, uint32_t nbs) {
     if (g.K == 0 || ((uint64_t)g.K * es) % 256 != 0) return 0;
@@ -196,51 +196,64 @@ uint32_t narrow_nb(const VkfGemmArgs &g, uint32_t batch, uint32_t es, uint32_t n
     return 0;
 }
 
+// The narrow-tile kernel for this product (nb set), VKF_K_COUNT if none: a
+// grid of fewer 128 x 128 tiles than CUs, operands the direct-to-LDS loads
+// take (checked here on the host: not for per-batch pointer arrays, which
+// live on the device), whole pairs of 128-byte K steps.  NN (fp16 Y stored
+// [K, C]) stages Y's k-rows as they lie and reads them back transposed, and
+// skips the 48-column tiles (512x3072x1024 NN 12.9 us on 128 x 64, 13.6 on
+// 128 x 48).
+static VkfKernelId narrow_kernel(const VkfGemmArgs &g, uint32_t batch, VkfKernelId id, uint32_t &nb) {
+    nb = 0;
+    const uint64_t tiles = (uint64_t)((g.Cn + 127) / 128) * ((g.R + 127) / 128) * batch;
+    if ((id != VKF_K_GEMM_F16 && id != VKF_K_GEMM_I8) || (g.flags & VKF_GF_X_F16Q) || g.bpx ||
+        tiles > (uint64_t)cu_count() || (batch > 1 && ((g.bsx | g.bsy) & 15) != 0))
+        return VKF_K_COUNT;
+    const uint32_t es = id == VKF_K_GEMM_F16 ? 2 : 1;
+    const bool xd = dma_operand(g.X, g.ldx, (g.flags & VKF_GF_X_TRANS) != 0, g.K, es);
+    if (xd && dma_operand(g.Y, g.ldy, (g.flags & VKF_GF_Y_TRANS) != 0, g.K, es)) {
+        static const VkfKernelId nk[2][5] = {
+            {VKF_K_GEMM_I8_N1, VKF_K_GEMM_I8_N2, VKF_K_GEMM_I8_N3, VKF_K_GEMM_I8_N4, VKF_K_GEMM_I8_N5},
+            {VKF_K_GEMM_F16_N1, VKF_K_GEMM_F16_N2, VKF_K_GEMM_F16_N3, VKF_K_GEMM_F16_N4, VKF_K_GEMM_F16_N5}};
+        nb = narrow_nb(g, batch, es, kNarrowAll);
+        return nb ? nk[es - 1][nb - 1] : VKF_K_COUNT;
+    }
+    if (id == VKF_K_GEMM_F16 && (g.flags & VKF_GF_Y_TRANS) && xd && (g.ldy * 2) % 16 == 0 &&
+        ((uintptr_t)g.Y & 15) == 0 && g.Cn % 8 == 0) {
+        static const VkfKernelId nt[5] = {VKF_K_GEMM_F16_N1T, VKF_K_GEMM_F16_N2T, VKF_K_GEMM_F16_N4T,
+                                          VKF_K_GEMM_F16_N4T, VKF_K_GEMM_F16_N5T};  // nb = 3 not taken
+        nb = narrow_nb(g, batch, 2, kNarrowAll & ~(1u << 3));
+        return nb ? nt[nb - 1] : VKF_K_COUNT;
+    }
+    return VKF_K_COUNT;
+}
+
 hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream, uint32_t batch) {
     if (g.R == 0 || g.Cn == 0 || batch == 0) return hipSuccess;
     dim3 grid((g.Cn + 127) / 128, (g.R + 127) / 128, batch);
     if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
-    // at most 64 rows: Y streamed once by 16-column workgroups
-    if (id == VKF_K_GEMM_F16 && skinny_ok(g, batch))
+    uint32_t nb = 0;
+    const VkfKernelId nk = narrow_kernel(g, batch, id, nb);
+    // at most 32 rows, or 64 where no narrow tiles apply: Y streamed once by
+    // 16-column workgroups (fp16 4096x4096 NT M = 48 / 64: 22.0 / 25.3 us
+    // streamed, 18.6 us on the narrow kernel's 128 x 16 tiles; M = 32 17.3)
+    if (id == VKF_K_GEMM_F16 && skinny_ok(g, batch) && (g.R <= 32 || nk == VKF_K_COUNT))
         return launch(VKF_K_GEMM_F16_SKINNY, dim3((g.Cn + 15) / 16, 1, batch), dim3(1024), &g, sizeof(g), stream,
                       131072);
-    // the split-K kernels need operands the direct-to-LDS loads take, checked
-    // here on the host: not for per-batch pointer arrays, which live on the device
+    // narrow tiles (128 x 16·nb) where they give the CUs more of the grid:
+    // the narrowest whose grid still fits one tile per CU
+    if (nk != VKF_K_COUNT)
+        return launch(nk, dim3((g.Cn + 16 * nb - 1) / (16 * nb), grid.y, batch), dim3(512), &g, sizeof(g), stream,
+                      kNarrowStages * 2 * (16384 + nb * 16 * 128));
+    // otherwise on such grids with K-contiguous operands: the split-K kernels
     if ((id == VKF_K_GEMM_F16 || id == VKF_K_GEMM_I8) && !(g.flags & VKF_GF_X_F16Q) && !g.bpx &&
         (uint64_t)grid.x * grid.y * batch <= (uint64_t)cu_count() &&
         (batch == 1 || ((g.bsx | g.bsy) & 15) == 0)) {
         const uint32_t es = id == VKF_K_GEMM_F16 ? 2 : 1;
         if (dma_operand(g.X, g.ldx, (g.flags & VKF_GF_X_TRANS) != 0, g.K, es) &&
-            dma_operand(g.Y, g.ldy, (g.flags & VKF_GF_Y_TRANS) != 0, g.K, es)) {
-            // narrow tiles (128 x 16·nb) where they give the CUs more of the
-            // grid: the narrowest whose grid still fits one tile per CU
-            const uint32_t nb = narrow_nb(g, batch, es, kNarrowAll);
-            if (nb) {
-                static const VkfKernelId nk[2][5] = {
-                    {VKF_K_GEMM_I8_N1, VKF_K_GEMM_I8_N2, VKF_K_GEMM_I8_N3, VKF_K_GEMM_I8_N4, VKF_K_GEMM_I8_N5},
-                    {VKF_K_GEMM_F16_N1, VKF_K_GEMM_F16_N2, VKF_K_GEMM_F16_N3, VKF_K_GEMM_F16_N4, VKF_K_GEMM_F16_N5}};
-                const dim3 gn((g.Cn + 16 * nb - 1) / (16 * nb), grid.y, batch);
-                return launch(nk[es - 1][nb - 1], gn, dim3(512), &g, sizeof(g), stream,
-                              kNarrowStages * 2 * (16384 + nb * 16 * 128));
-            }
+            dma_operand(g.Y, g.ldy, (g.flags & VKF_GF_Y_TRANS) != 0, g.K, es))
             return launch(id == VKF_K_GEMM_F16 ? VKF_K_GEMM_F16_K2 : VKF_K_GEMM_I8_K2, grid, dim3(512), &g,
                           sizeof(g), stream);
-        }
-        // fp16 with Y stored [K, C] (NN): the narrow kernel's tiles with Y's
-        // k-rows staged as they lie and read back transposed
-        if (id == VKF_K_GEMM_F16 && (g.flags & VKF_GF_Y_TRANS) &&
-            dma_operand(g.X, g.ldx, (g.flags & VKF_GF_X_TRANS) != 0, g.K, 2) && (g.ldy * 2) % 16 == 0 &&
-            ((uintptr_t)g.Y & 15) == 0 && g.Cn % 8 == 0) {
-            static const VkfKernelId nt[5] = {VKF_K_GEMM_F16_N1T, VKF_K_GEMM_F16_N2T, VKF_K_GEMM_F16_N4T,
-                                              VKF_K_GEMM_F16_N4T, VKF_K_GEMM_F16_N5T};  // nb = 3 not taken
-            // (not the 48-column tiles: 512x3072x1024 NN 12.9 us on 128 x 64,
-            // 13.6 on 128 x 48)
-            const uint32_t nb = narrow_nb(g, batch, 2, kNarrowAll & ~(1u << 3));
-            if (nb)
-                return launch(nt[nb - 1],
-                              dim3((g.Cn + 16 * nb - 1) / (16 * nb), grid.y, batch), dim3(512), &g, sizeof(g), stream,
-                              kNarrowStages * 2 * (16384 + nb * 16 * 128));
-        }
     }
     // grids of at least one 256 x 256 tile per CU, both operands K-contiguous:
     // the 256 x 256 kernel (half the tile bytes per MAC).  int8 gains on every
