@@ -48,14 +48,16 @@ def test_linear_fp16_nn_transposed_reads(dev, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 136, 96), (16, 8, 32), (17, 520, 1024), (32, 4096, 4096),
-                                   (33, 200, 4128), (64, 1000, 288), (48, 4096, 4096), (64, 1000, 256)])
+                                   (33, 200, 4128), (64, 1000, 288), (48, 4096, 4096), (64, 1000, 256),
+                                   (1, 11008, 1024), (16, 11008, 1024)])
 @pytest.mark.parametrize("transB", [1, 0])
 def test_linear_fp16_skinny(dev, M, N, K, transB):
-    """At most 32 rows of A, or 64 where the narrow-tile kernels do not
-    apply (K not whole pairs of 128-byte steps): the skinny kernel (B
-    streamed once by 16-column workgroups, K split over 16 waves, partial
-    tiles summed in wave order); 33 to 64 rows otherwise on the narrow
-    tiles (48 x 4096 x 4096, 64 x 1000 x 256).  B [N, K] or [K, N]; fp32
+    """Few rows of A: the skinny kernel (B streamed once by 16-column
+    workgroups, K split over 16 waves, partial tiles summed in wave order)
+    up to 64 rows where the narrow-tile kernels do not apply (K not whole
+    pairs of 128-byte steps), else up to 8 rows, and up to 32 while its
+    workgroups fit one per CU; the narrow tiles otherwise (48 x 4096 x
+    4096, 64 x 1000 x 256, 16 x 11008 x 1024).  B [N, K] or [K, N]; fp32
     out, then fp16 out with alpha, beta*C and an activation, checked
     against the same float64 product."""
     import torch

@@ -234,10 +234,16 @@ hipError_t launch_gemm(VkfKernelId id, const VkfGemmArgs &g, hipStream_t stream,
     if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
     uint32_t nb = 0;
     const VkfKernelId nk = narrow_kernel(g, batch, id, nb);
-    // at most 32 rows, or 64 where no narrow tiles apply: Y streamed once by
-    // 16-column workgroups (fp16 4096x4096 NT M = 48 / 64: 22.0 / 25.3 us
-    // streamed, 18.6 us on the narrow kernel's 128 x 16 tiles; M = 32 17.3)
-    if (id == VKF_K_GEMM_F16 && skinny_ok(g, batch) && (g.R <= 32 || nk == VKF_K_COUNT))
+    // at most 64 rows: Y streamed once by 16-column workgroups where no
+    // narrow tiles apply, else up to 8 rows, and up to 32 while those
+    // workgroups fit one per CU (same-process A/B, fp16 cold B, streamed
+    // against narrow tiles: 4096x4096 NT M = 8 / 16 / 48 / 64 10.8 / 12.4 /
+    // 22.2 / 25.5 against 19.1 / 19.0 / 19.0 / 18.9 us, NN M = 32 24.7
+    // against 26.6; 11008x4096 NT M = 1 / 16 / 32 21.6 / 32.3 / 46.1
+    // against 25.9 / 26.0 / 26.3 us, 688 streaming workgroups)
+    const bool sk_fits = (uint64_t)((g.Cn + 15) / 16) * batch <= (uint64_t)cu_count();
+    if (id == VKF_K_GEMM_F16 && skinny_ok(g, batch) &&
+        (nk == VKF_K_COUNT || g.R <= 8 || (g.R <= 32 && sk_fits)))
         return launch(VKF_K_GEMM_F16_SKINNY, dim3((g.Cn + 15) / 16, 1, batch), dim3(1024), &g, sizeof(g), stream,
                       131072);
     // narrow tiles (128 x 16·nb) where they give the CUs more of the grid:
