@@ -336,6 +336,18 @@ def test_gemv_mfma_k_slices(dev, qt, K, M, N):
     assert max(rel_err(a[m], y_seq.cpu().numpy()[m]) for m in range(M)) <= TOL_F32
 
 
+@pytest.mark.parametrize("N", [1, 9, 16, 17])
+def test_gemv_mfma_k_slices_few_rows(dev, N):
+    """K slices with a single (ragged) 16-row tile or two: one workgroup per
+    slice, the rows past N of the tile clamped to the last row."""
+    from vkflame_amd import ops
+    K, M = 13824, 6
+    w = O.gen_weight(O.Q4_K, N, K, seed_for(2, 150 + N))
+    xa, x64 = _x("f16", M, K, seed_for(2, 151))
+    y = ops.gemm_q(to_dev(w, dev), O.Q4_K, to_dev(xa, dev), N, K).cpu().numpy()
+    assert _per_row_err(y, x64, w, O.Q4_K, N, K) <= TOL_F32
+
+
 def test_gemv_mfma_k_slices_strided_output(dev):
     """The slice sum writes y at its row stride and leaves the padding."""
     import torch
