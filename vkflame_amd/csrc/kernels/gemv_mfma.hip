@@ -830,8 +830,8 @@ VKF_GEMV_MFMA(q5_0, GF_Q5_0)
 // sub-block sums of x for the min-term MFMA, added across the lane pair
 // that shares each sub-block).  The workgroup walks its tiles one per
 // round: a wave multiplies its groups of the round's tile, requests the
-// next round's weights, and the P partial tiles meet in LDS, where wave 0
-// adds them in wave order.  Rows >= M of the MFMA operand repeat row M - 1
+// next round's weights, and the P partial tiles meet in LDS, where waves
+// 0..3 each add one of the four elements per lane in wave order.  Rows >= M of the MFMA operand repeat row M - 1
 // (MR = M rounded up to 4, 8 or 16) and feed discarded outputs.
 //
 // K slices (KS, for K longer than P waves hold): the S = flags bits 8..15
@@ -909,7 +909,7 @@ __device__ __forceinline__ void gemv_mfma_xr(const VkfGemvArgs &a, unsigned char
     };
     uint32_t c64 = 0x64006400u;
     asm volatile("" : "+v"(c64));
-    float *red = (float *)smem;  // [P waves][64 lanes][4]
+    float *red = (float *)smem;  // [P waves][4 elements][64 lanes]
     const vkf_f4 zero = {0, 0, 0, 0};
     auto round = [&](uint32_t tile, GmSb<F> *cur) {
         vkf_f4 y4 = zero;
@@ -926,26 +926,20 @@ __device__ __forceinline__ void gemv_mfma_xr(const VkfGemvArgs &a, unsigned char
         }
         // the next round's weights load under the reduction
         if (tile + tstep() < ntiles && ng > 0) load_round(tile + tstep(), cur);
-        *(vkf_f4 *)(red + (wave * 64 + lane) * 4) = y4;
+#pragma unroll
+        for (int e = 0; e < 4; e++) red[(wave * 4 + e) * 64 + lane] = y4[e];
         __syncthreads();
-        if (wave == 0) {
-            vkf_f4 s = y4;
-            for (int w = 1; w < P; w++) {
-                const vkf_f4 v = *(const vkf_f4 *)(red + (w * 64 + lane) * 4);
-#pragma unroll
-                for (int e = 0; e < 4; e++) s[e] += v[e];
-            }
-            const uint32_t n = tile * 16 + li;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t m = 4 * lg + e;
-                if (m < a.M && n < a.N) {
-                    if constexpr (KS) {
-                        a.y[((uint64_t)slice * a.M + m) * a.ldy + n] = s[e];
-                    } else {
-                        float *yp = a.y + (uint64_t)m * a.ldy + n;
-                        *yp = (a.flags & 1u) ? *yp + s[e] : s[e];
-                    }
+        if (wave < 4) {  // wave e adds element e of the P partial tiles, in wave order
+            const int e = wave;
+            float s = red[e * 64 + lane];
+            for (int w = 1; w < P; w++) s += red[(w * 4 + e) * 64 + lane];
+            const uint32_t n = tile * 16 + li, m = 4 * lg + e;
+            if (m < a.M && n < a.N) {
+                if constexpr (KS) {
+                    a.y[((uint64_t)slice * a.M + m) * a.ldy + n] = s;
+                } else {
+                    float *yp = a.y + (uint64_t)m * a.ldy + n;
+                    *yp = (a.flags & 1u) ? *yp + s : s;
                 }
             }
         }
